@@ -1,0 +1,240 @@
+/*
+ * mvllm_amd.h — C ABI of the MI355X (gfx950) ragged paged-attention library.
+ *
+ * The library implements the tensor work of micro-vLLM's attention operator
+ * (src/micro_vllm/attention/operators/base.py:30-40) as hand-written HIP
+ * kernels: the paged KV-cache write, ragged causal GQA attention over the
+ * paged cache (split-KV decode and MFMA prefill), a bit-exact block gather,
+ * and the ragged-batch packing that the reference ModelRunner performs in
+ * Python loops.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer unless noted; every size and stride is
+ *    in elements (not bytes) and is a plain int64_t.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Calls only enqueue work: nothing synchronises with the host, nothing is
+ *    allocated, so every entry point may be recorded into a HIP graph.
+ *  - Return value: 0 on success, a negative MVLLM_ERR_* code on failure;
+ *    mvllm_last_error() then describes the failure (thread-local text).
+ *  - Index tensors are int64, as in the reference (AttentionMetadata,
+ *    attention.py:12-28). Padding conventions follow the reference: slot -1
+ *    writes nothing; a request with an empty query range does nothing;
+ *    tokens outside every request get zero output; block-table entries past a
+ *    request's visible context are never read.
+ *  - The paged cache is the reference's tensor of shape
+ *    (2, num_blocks, block_size, num_kv_heads, head_dim): plane 0 holds keys,
+ *    plane 1 values (model_runner.py:688-703).
+ */
+#ifndef MVLLM_AMD_H
+#define MVLLM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (torch.float32 / torch.float16 / torch.bfloat16). */
+enum {
+  MVLLM_DTYPE_F32 = 0,
+  MVLLM_DTYPE_F16 = 1,
+  MVLLM_DTYPE_BF16 = 2
+};
+
+/* Status codes. */
+enum {
+  MVLLM_OK = 0,
+  MVLLM_ERR_INVALID = -1,     /* bad shape, stride, pointer or size */
+  MVLLM_ERR_UNSUPPORTED = -2, /* dtype / geometry this build does not handle */
+  MVLLM_ERR_HIP = -3,         /* a HIP runtime call failed */
+  MVLLM_ERR_WORKSPACE = -4    /* workspace smaller than required */
+};
+
+/* Attention visibility kinds (spec.py:13-51). */
+enum {
+  MVLLM_SPEC_FULL = 0,           /* start = 0 */
+  MVLLM_SPEC_SLIDING_WINDOW = 1, /* start = max(0, pos - window + 1) */
+  MVLLM_SPEC_CHUNKED_LOCAL = 2   /* start = (pos / chunk) * chunk */
+};
+
+/* A strided [tokens, heads, dim] device tensor (query, key, value, output). */
+typedef struct mvllm_tensor3 {
+  void* data;
+  int32_t dtype;
+  int32_t reserved;
+  int64_t size[3];
+  int64_t stride[3];
+} mvllm_tensor3;
+
+/* The paged cache (2, num_blocks, block_size, num_kv_heads, head_dim). */
+typedef struct mvllm_kv_cache {
+  void* data;
+  int32_t dtype;
+  int32_t reserved;
+  int64_t num_blocks;
+  int64_t block_size;
+  int64_t num_kv_heads;
+  int64_t head_dim;
+  int64_t stride[5];
+} mvllm_kv_cache;
+
+/* AttentionMetadata (attention.py:12-28) as device int64 arrays. */
+typedef struct mvllm_batch {
+  const int64_t* query_positions;               /* [num_tokens] */
+  const int64_t* query_context_start_positions; /* [num_tokens] */
+  const int64_t* query_start_locations;         /* [num_requests + 1] */
+  const int64_t* context_lengths;               /* [num_requests] */
+  const int64_t* block_table;                   /* [num_requests, width] */
+  const int64_t* slot_mapping;                  /* [num_tokens] */
+  int64_t num_tokens;
+  int64_t num_requests;
+  int64_t block_table_width;
+  int64_t block_table_stride[2];
+  int64_t block_size;
+} mvllm_batch;
+
+/*
+ * Scatter key/value rows into their physical cache slots:
+ *   cache[0|1, slot / block_size, slot % block_size, h, :] = key|value[t, h, :]
+ * Bit-exact copy; slot < 0 (padding) and slot >= num_blocks * block_size
+ * write nothing. Slots must be distinct (the KV-cache manager guarantees it).
+ * Replaces write_kv_cache (reference.py:84-98) and triton_write_kv_cache /
+ * _write_kv_cache_kernel (triton_paged.py:293-325, 11-68).
+ */
+int mvllm_kv_write(const mvllm_tensor3* key, const mvllm_tensor3* value,
+                   const mvllm_kv_cache* cache, const int64_t* slot_mapping,
+                   int64_t num_tokens, void* stream);
+
+/*
+ * Bytes of device workspace mvllm_paged_attention / mvllm_attention_forward
+ * need for this batch geometry (split-KV partial results). Depends only on
+ * shapes, never on device data, so it can be sized before graph capture.
+ */
+int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch,
+                                        int64_t num_q_heads, int64_t head_dim);
+
+/*
+ * Ragged causal GQA attention over the paged cache (the cache must already
+ * hold every visible key, including the batch's own tokens). For query t of
+ * request r, key positions [max(start(t), start(first query of r)),
+ * min(pos(t), context_length(r) - 1)] are visible; softmax(q.k * scale) . v
+ * in fp32, written in out's dtype. Tokens outside every request get zeros.
+ * Replaces the attention part of ReferenceAttentionOperator.forward
+ * (reference.py:26-81) and triton_paged_attention / _paged_attention_kernel
+ * (triton_paged.py:328-389, 97-290).
+ */
+int mvllm_paged_attention(const mvllm_tensor3* query,
+                          const mvllm_kv_cache* cache,
+                          const mvllm_batch* batch, const mvllm_tensor3* out,
+                          float scale, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/*
+ * The whole operator: mvllm_kv_write(key, value, slot_mapping) followed by
+ * mvllm_paged_attention. Replaces AttentionOperator.forward
+ * (base.py:30-40) as implemented by ReferenceAttentionOperator.forward
+ * (reference.py:14-81) and TritonPagedAttentionOperator.forward
+ * (triton_paged.py:395-418).
+ */
+int mvllm_attention_forward(const mvllm_tensor3* query,
+                            const mvllm_tensor3* key,
+                            const mvllm_tensor3* value,
+                            const mvllm_kv_cache* cache,
+                            const mvllm_batch* batch, const mvllm_tensor3* out,
+                            float scale, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/*
+ * Bit-exact gather of each request's visible K/V history into padded,
+ * contiguous [num_requests, capacity, num_kv_heads, head_dim] buffers (same
+ * dtype as the cache): row i of request r is the cache row of position
+ * start(first query of r) + i, for i < context_length(r) - that start; rows
+ * past it are left untouched. Replaces gather_kv_cache (reference.py:101-138);
+ * the padded layout is the one of the reference's teaching gather kernel
+ * (benchmarks/spike_triton_paged.py:52-174).
+ */
+int mvllm_gather_kv(const mvllm_kv_cache* cache, const mvllm_batch* batch,
+                    int64_t capacity, void* out_key, void* out_value,
+                    void* stream);
+
+/*
+ * Per-query visibility start for an attention spec:
+ *   out[i] = start(positions[i]) for spec kind `spec_kind` with parameter
+ *   `spec_parameter` (window size or chunk size; ignored for FULL).
+ * Replaces the host loop in Attention.build_metadata (attention.py:68-75)
+ * over AttentionSpec.context_start (spec.py:13-51).
+ */
+int mvllm_context_starts(const int64_t* positions, int64_t num_tokens,
+                         int32_t spec_kind, int64_t spec_parameter,
+                         int64_t* out, void* stream);
+
+/*
+ * Ragged-batch packing on the GPU. Input is a compact per-step payload in
+ * device memory (int32, MVLLM_PACK_FIELDS values per request):
+ *   request_info[r * 8 + 0] = num_computed_tokens
+ *   request_info[r * 8 + 1] = num_scheduled_tokens
+ *   request_info[r * 8 + 2] = number of block ids of request r (this group)
+ *   request_info[r * 8 + 3] = 1 if the request requires sampling, else 0
+ *   request_info[r * 8 + 4 .. 7] = scratch, overwritten by the call (the
+ *                                  per-request prefix sums)
+ *   block_ids   = concatenation of every request's block ids (this group)
+ *   token_ids   = concatenation of every request's input token ids (may be
+ *                 NULL when input_ids is NULL)
+ * Outputs (int64, NULL = not wanted) are written at the given capacities,
+ * padded exactly as a captured graph expects (model_runner.py:78-122):
+ *   input_ids[token_capacity]       (pad 0)
+ *   positions[token_capacity]       (pad 0)
+ *   context_starts[token_capacity]  (pad 0)
+ *   query_start_locations[request_capacity + 1] (pad num_tokens)
+ *   context_lengths[request_capacity]           (pad 0)
+ *   block_table[request_capacity, block_table_width] (pad null_block_id)
+ *   slot_mapping[token_capacity]    (pad -1; also -1 for a position whose
+ *                                    logical block has no block id)
+ *   sampling_rows[num_sampling]     (last flattened row of each sampling
+ *                                    request, in request order)
+ * With capacities equal to the actual sizes this is the unpadded output of
+ * ModelRunner._flatten_model_input / _build_slot_mapping / _build_block_table
+ * (model_runner.py:751-900) plus Attention.build_metadata's context starts.
+ */
+typedef struct mvllm_pack_args {
+  int32_t* request_info;
+  const int32_t* block_ids;
+  const int32_t* token_ids;
+  int64_t num_requests;
+  int64_t num_tokens;
+  int64_t num_block_ids;
+  int64_t block_size;
+  int64_t null_block_id;
+  int32_t spec_kind;
+  int32_t reserved;
+  int64_t spec_parameter;
+  int64_t token_capacity;
+  int64_t request_capacity;
+  int64_t block_table_width;
+  int64_t* input_ids;
+  int64_t* positions;
+  int64_t* context_starts;
+  int64_t* query_start_locations;
+  int64_t* context_lengths;
+  int64_t* block_table;
+  int64_t* slot_mapping;
+  int64_t* sampling_rows;
+} mvllm_pack_args;
+
+#define MVLLM_PACK_FIELDS 8
+
+int mvllm_pack_batch(const mvllm_pack_args* args, void* stream);
+
+/* Text of the last failure on this thread ("" if none). */
+const char* mvllm_last_error(void);
+
+/* ABI version of this header (bumped on incompatible change). */
+int mvllm_abi_version(void);
+
+#define MVLLM_ABI_VERSION 1
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MVLLM_AMD_H */

@@ -1,0 +1,72 @@
+// Internal interface shared by the attention kernels.
+#pragma once
+
+#include "common.h"
+
+namespace mvllm {
+
+// Everything a ragged paged-attention launch needs. Strides are in elements.
+struct AttnArgs {
+  const void* q;
+  int64_t q_s0, q_s1, q_s2;
+  const void* cache;
+  int64_t c_s[5];
+  void* out;
+  int64_t o_s0, o_s1, o_s2;
+  const int64_t* positions;
+  const int64_t* cstarts;
+  const int64_t* qsl;
+  const int64_t* lengths;
+  const int64_t* table;
+  int64_t t_s0, t_s1, width;
+  int64_t num_tokens, num_requests, num_blocks, block_size;
+  int32_t num_q_heads, num_kv_heads, group, head_dim;
+  float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
+  // Split-KV decode partials: acc [R][max_splits][Hq][D], (max, sum) [R][max_splits][Hq].
+  float* ws_acc;
+  float2* ws_ml;
+  int32_t split_tokens, max_splits;
+  int32_t mode;  // generic kernel: 0 = every token; 1 = only requests with > 1 query
+};
+
+// Visible key positions [lo, hi] of query `t` in request `r` whose first
+// query is `qs`: the reference gathers [start(first query), length) and
+// masks keys outside [start(t), pos(t)] (reference.py:101-138, 49-68).
+// Positions past the block table's reach cannot be mapped and are clipped.
+__device__ __forceinline__ void visible_range(const AttnArgs& a, int64_t r, int64_t qs,
+                                              int64_t t, int64_t& lo, int64_t& hi) {
+  const int64_t first = a.cstarts[qs];
+  const int64_t own = a.cstarts[t];
+  lo = own > first ? own : first;
+  if (lo < 0) lo = 0;
+  hi = a.positions[t];
+  const int64_t last = a.lengths[r] - 1;
+  if (last < hi) hi = last;
+  const int64_t reach = a.width * a.block_size - 1;
+  if (reach < hi) hi = reach;
+}
+
+// Physical block holding position p of request r, or -1 when the table
+// entry is not a valid block id (such keys are treated as masked).
+__device__ __forceinline__ int64_t block_of(const AttnArgs& a, int64_t r, int64_t p) {
+  const int64_t b = a.table[r * a.t_s0 + (p / a.block_size) * a.t_s1];
+  return (b >= 0 && b < a.num_blocks) ? b : -1;
+}
+
+// Number of split-KV partitions of a decode query with visible range [lo, hi].
+__device__ __forceinline__ int64_t decode_num_splits(int64_t lo, int64_t hi, int32_t split) {
+  if (hi < lo) return 0;
+  const int64_t base = lo & ~int64_t(15);
+  return (hi - base + split) / split;
+}
+
+// Host-side launchers (one per kernel family).
+int launch_generic(const AttnArgs& a, int32_t dtype, hipStream_t s);
+int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s);
+int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s);
+bool prefill_supported(const AttnArgs& a, int32_t dtype);
+
+// Device properties used for launch shapes (cached per device).
+int device_cu_count();
+
+}  // namespace mvllm

@@ -1,0 +1,201 @@
+// C-ABI entry points of ragged paged attention: validation, workspace
+// sizing and dispatch to the decode / prefill / generic kernels.
+#include <cmath>
+#include <cstdlib>
+#include <mutex>
+
+#include "attention.h"
+
+namespace mvllm {
+
+int device_cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+namespace {
+
+// Split size (tokens) of the split-KV decode partition. It depends only on
+// shapes so that the workspace can be sized before a graph is captured.
+int32_t decode_split_tokens(int64_t num_requests, int64_t max_context) {
+  if (const char* env = std::getenv("MVLLM_DECODE_SPLIT")) {
+    const long v = std::strtol(env, nullptr, 10);
+    if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) return static_cast<int32_t>(v);
+  }
+  // Aim for roughly 8 (request, split) items per CU when every request
+  // reaches half of the table's reach; never below 64 tokens per split.
+  const int64_t target_items = 8LL * device_cu_count();
+  const int64_t est_tokens = num_requests * (max_context / 2 > 16 ? max_context / 2 : 16);
+  int64_t split = (est_tokens + target_items - 1) / target_items;
+  split = (split + 15) / 16 * 16;
+  if (split < 64) split = 64;
+  if (split > 4096) split = 4096;
+  return static_cast<int32_t>(split);
+}
+
+struct DecodeLayout {
+  int32_t split_tokens;
+  int32_t max_splits;
+  int64_t acc_bytes;
+  int64_t ml_bytes;
+};
+
+DecodeLayout decode_layout(const mvllm_batch* b, int64_t num_q_heads, int64_t head_dim) {
+  DecodeLayout d;
+  const int64_t reach = b->block_table_width * b->block_size;
+  d.split_tokens = decode_split_tokens(b->num_requests, reach);
+  // Visible ranges start at a 16-aligned base at most 15 tokens early.
+  const int64_t splits = (reach + 15 + d.split_tokens) / d.split_tokens;
+  d.max_splits = static_cast<int32_t>(splits < 1 ? 1 : splits);
+  const int64_t items = b->num_requests * d.max_splits * num_q_heads;
+  d.acc_bytes = (items * head_dim * 4 + 255) / 256 * 256;
+  d.ml_bytes = (items * 8 + 255) / 256 * 256;
+  return d;
+}
+
+int check_tensor(const mvllm_tensor3* t, const char* name) {
+  if (!t) return fail(MVLLM_ERR_INVALID, "%s descriptor is null", name);
+  if (dtype_bytes(t->dtype) == 0) return fail(MVLLM_ERR_UNSUPPORTED, "%s has unsupported dtype", name);
+  for (int i = 0; i < 3; ++i)
+    if (t->size[i] < 0 || t->stride[i] < 0)
+      return fail(MVLLM_ERR_INVALID, "%s has a negative size or stride", name);
+  if (t->size[0] > 0 && t->size[1] > 0 && t->size[2] > 0 && !t->data)
+    return fail(MVLLM_ERR_INVALID, "%s data pointer is null", name);
+  return MVLLM_OK;
+}
+
+int check_batch(const mvllm_batch* b, const mvllm_kv_cache* c) {
+  if (!b) return fail(MVLLM_ERR_INVALID, "batch is null");
+  if (b->num_tokens < 0 || b->num_requests < 0 || b->block_table_width < 0)
+    return fail(MVLLM_ERR_INVALID, "negative batch size");
+  if (b->block_size != c->block_size)
+    return fail(MVLLM_ERR_INVALID, "metadata block_size %lld != cache block_size %lld",
+                (long long)b->block_size, (long long)c->block_size);
+  if (!b->query_start_locations) return fail(MVLLM_ERR_INVALID, "query_start_locations is null");
+  if (b->num_tokens > 0 && (!b->query_positions || !b->query_context_start_positions))
+    return fail(MVLLM_ERR_INVALID, "query_positions/context starts are null");
+  if (b->num_requests > 0 && (!b->context_lengths || (b->block_table_width > 0 && !b->block_table)))
+    return fail(MVLLM_ERR_INVALID, "context_lengths/block_table are null");
+  return MVLLM_OK;
+}
+
+bool vec16(int64_t stride_elems, int64_t esize) { return (stride_elems * esize) % 16 == 0; }
+
+}  // namespace
+}  // namespace mvllm
+
+using namespace mvllm;
+
+extern "C" int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch, int64_t num_q_heads,
+                                                   int64_t head_dim) {
+  if (!batch || num_q_heads <= 0 || head_dim <= 0 || batch->num_requests <= 0 ||
+      batch->block_size <= 0)
+    return 0;
+  const DecodeLayout d = decode_layout(batch, num_q_heads, head_dim);
+  return d.acc_bytes + d.ml_bytes;
+}
+
+extern "C" int mvllm_paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
+                                     const mvllm_batch* batch, const mvllm_tensor3* out,
+                                     float scale, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  clear_error();
+  if (int rc = check_tensor(query, "query")) return rc;
+  if (int rc = check_tensor(out, "out")) return rc;
+  if (!cache || !cache->data) return fail(MVLLM_ERR_INVALID, "cache is null");
+  if (int rc = check_batch(batch, cache)) return rc;
+  const int32_t dtype = query->dtype;
+  if (cache->dtype != dtype || out->dtype != dtype)
+    return fail(MVLLM_ERR_INVALID, "query/cache/out dtypes differ (%s/%s/%s)", dtype_name(dtype),
+                dtype_name(cache->dtype), dtype_name(out->dtype));
+  const int64_t N = batch->num_tokens;
+  const int64_t Hq = query->size[1], D = query->size[2], Hkv = cache->num_kv_heads;
+  if (query->size[0] != N || out->size[0] != N || out->size[1] != Hq || out->size[2] != D)
+    return fail(MVLLM_ERR_INVALID, "query/out shapes do not match [%lld, %lld, %lld]",
+                (long long)N, (long long)Hq, (long long)D);
+  if (cache->head_dim != D) return fail(MVLLM_ERR_INVALID, "cache head_dim %lld != query head_dim %lld",
+                                        (long long)cache->head_dim, (long long)D);
+  if (Hkv <= 0 || Hq % Hkv != 0)
+    return fail(MVLLM_ERR_INVALID, "query heads %lld not a multiple of KV heads %lld",
+                (long long)Hq, (long long)Hkv);
+  if (N == 0) return MVLLM_OK;
+  if (Hq > 65535 || D > 65535) return fail(MVLLM_ERR_INVALID, "head count or head_dim too large");
+
+  AttnArgs a = {};
+  a.q = query->data;
+  a.q_s0 = query->stride[0]; a.q_s1 = query->stride[1]; a.q_s2 = query->stride[2];
+  a.cache = cache->data;
+  for (int i = 0; i < 5; ++i) a.c_s[i] = cache->stride[i];
+  a.out = out->data;
+  a.o_s0 = out->stride[0]; a.o_s1 = out->stride[1]; a.o_s2 = out->stride[2];
+  a.positions = batch->query_positions;
+  a.cstarts = batch->query_context_start_positions;
+  a.qsl = batch->query_start_locations;
+  a.lengths = batch->context_lengths;
+  a.table = batch->block_table;
+  a.t_s0 = batch->block_table_stride[0];
+  a.t_s1 = batch->block_table_stride[1];
+  a.width = batch->block_table_width;
+  a.num_tokens = N;
+  a.num_requests = batch->num_requests;
+  a.num_blocks = cache->num_blocks;
+  a.block_size = cache->block_size;
+  a.num_q_heads = static_cast<int32_t>(Hq);
+  a.num_kv_heads = static_cast<int32_t>(Hkv);
+  a.group = static_cast<int32_t>(Hq / Hkv);
+  a.head_dim = static_cast<int32_t>(D);
+  a.scale_log2 = scale * 1.4426950408889634f;  // log2(e)
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  const int64_t es = dtype_bytes(dtype);
+  const bool fast = (dtype == MVLLM_DTYPE_BF16 || dtype == MVLLM_DTYPE_F16) && D == 128 &&
+                    a.group <= 16 && cache->stride[4] == 1 && cache->stride[3] == D &&
+                    vec16(cache->stride[0], es) && vec16(cache->stride[1], es) &&
+                    vec16(cache->stride[2], es) && aligned16(cache->data) &&
+                    query->stride[2] == 1 && vec16(query->stride[0], es) &&
+                    vec16(query->stride[1], es) && aligned16(query->data) && out->stride[2] == 1 &&
+                    vec16(out->stride[0], es) && vec16(out->stride[1], es) && aligned16(out->data);
+  if (!fast || a.num_requests == 0) {
+    a.mode = 0;
+    return launch_generic(a, dtype, s);
+  }
+  const DecodeLayout d = decode_layout(batch, Hq, D);
+  if (workspace_bytes < d.acc_bytes + d.ml_bytes || (!workspace && d.acc_bytes + d.ml_bytes > 0))
+    return fail(MVLLM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld required",
+                (long long)workspace_bytes, (long long)(d.acc_bytes + d.ml_bytes));
+  if (!aligned16(workspace)) return fail(MVLLM_ERR_INVALID, "workspace must be 16-byte aligned");
+  a.split_tokens = d.split_tokens;
+  a.max_splits = d.max_splits;
+  a.ws_acc = static_cast<float*>(workspace);
+  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + d.acc_bytes);
+  if (int rc = launch_decode(a, dtype, s)) return rc;
+  if (prefill_supported(a, dtype)) return launch_prefill(a, dtype, s);
+  a.mode = 1;
+  return launch_generic(a, dtype, s);
+}
+
+extern "C" int mvllm_attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,
+                                       const mvllm_tensor3* value, const mvllm_kv_cache* cache,
+                                       const mvllm_batch* batch, const mvllm_tensor3* out,
+                                       float scale, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  clear_error();
+  if (!batch) return fail(MVLLM_ERR_INVALID, "batch is null");
+  if (batch->num_tokens > 0) {
+    if (!batch->slot_mapping) return fail(MVLLM_ERR_INVALID, "slot_mapping is null");
+    if (int rc = mvllm_kv_write(key, value, cache, batch->slot_mapping, batch->num_tokens, stream))
+      return rc;
+  }
+  return mvllm_paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, stream);
+}

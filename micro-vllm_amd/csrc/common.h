@@ -1,0 +1,193 @@
+// Shared host/device helpers of the gfx950 paged-attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "mvllm_amd.h"
+
+namespace mvllm {
+
+// ---------------------------------------------------------------- errors ----
+
+// Records the failure text for mvllm_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define MVLLM_HIP_TRY(expr)                                                   \
+  do {                                                                        \
+    hipError_t mvllm_status_ = (expr);                                        \
+    if (mvllm_status_ != hipSuccess)                                          \
+      return ::mvllm::fail(MVLLM_ERR_HIP, "%s failed: %s", #expr,             \
+                           hipGetErrorString(mvllm_status_));                 \
+  } while (0)
+
+// After a kernel launch: report a launch failure (bad configuration etc.).
+#define MVLLM_LAUNCH_CHECK(name)                                              \
+  do {                                                                        \
+    hipError_t mvllm_status_ = hipGetLastError();                             \
+    if (mvllm_status_ != hipSuccess)                                          \
+      return ::mvllm::fail(MVLLM_ERR_HIP, "launch of %s failed: %s", name,    \
+                           hipGetErrorString(mvllm_status_));                 \
+  } while (0)
+
+inline int64_t dtype_bytes(int32_t dtype) {
+  switch (dtype) {
+    case MVLLM_DTYPE_F32: return 4;
+    case MVLLM_DTYPE_F16: return 2;
+    case MVLLM_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+inline const char* dtype_name(int32_t dtype) {
+  switch (dtype) {
+    case MVLLM_DTYPE_F32: return "float32";
+    case MVLLM_DTYPE_F16: return "float16";
+    case MVLLM_DTYPE_BF16: return "bfloat16";
+    default: return "unknown";
+  }
+}
+
+inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// -------------------------------------------------------- element types ----
+
+// 16-bit storage types are carried as raw bits; arithmetic is always fp32.
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef short short8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quiet).
+__device__ __forceinline__ uint32_t float_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
+  _Float16 h;
+  uint16_t b = static_cast<uint16_t>(bits16);
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ uint32_t float_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);  // v_cvt_f16_f32: round to nearest even
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+template <typename T> struct Elem;
+
+template <> struct Elem<float> {
+  static constexpr int32_t code = MVLLM_DTYPE_F32;
+  __device__ static float load(const float* p) { return *p; }
+  __device__ static void store(float* p, float v) { *p = v; }
+};
+
+template <> struct Elem<bf16_t> {
+  static constexpr int32_t code = MVLLM_DTYPE_BF16;
+  __device__ static float load(const bf16_t* p) { return bf16_bits_to_float(p->bits); }
+  __device__ static void store(bf16_t* p, float v) {
+    p->bits = static_cast<uint16_t>(float_to_bf16_bits(v));
+  }
+  __device__ static float from_bits(uint32_t b) { return bf16_bits_to_float(b); }
+  __device__ static uint32_t to_bits(float v) { return float_to_bf16_bits(v); }
+};
+
+template <> struct Elem<f16_t> {
+  static constexpr int32_t code = MVLLM_DTYPE_F16;
+  __device__ static float load(const f16_t* p) { return f16_bits_to_float(p->bits); }
+  __device__ static void store(f16_t* p, float v) {
+    p->bits = static_cast<uint16_t>(float_to_f16_bits(v));
+  }
+  __device__ static float from_bits(uint32_t b) { return f16_bits_to_float(b); }
+  __device__ static uint32_t to_bits(float v) { return float_to_f16_bits(v); }
+};
+
+// ------------------------------------------------------- wave utilities ----
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+// Orders this wave's LDS writes before its later LDS reads (and vice versa)
+// without a workgroup barrier: the waves of one workgroup never share LDS
+// rows in the decode kernel.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---------------------------------------------------------------- MFMA ----
+//
+// gfx950 matrix cores, wave64. Operand layouts used throughout (lane l,
+// col = l % 16, grp = l / 16):
+//   16x16x32: A[m][k] lane holds m = col, k = 8*grp .. 8*grp+7
+//             B[k][n] lane holds n = col, k = 8*grp .. 8*grp+7
+//   16x16x16: A lane holds m = col, k = 4*grp .. 4*grp+3 (B likewise)
+//   C/D (16x16 fp32): lane holds n = col, m = 4*grp .. 4*grp+3
+// The kernels only rely on these layouts; they are checked on the device by
+// the MFMA layout test.
+
+template <typename T> struct Mfma;
+
+template <> struct Mfma<bf16_t> {
+  __device__ static float4_t k32(short8_t a, short8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(__attribute__((ext_vector_type(8))) __bf16, a),
+        __builtin_bit_cast(__attribute__((ext_vector_type(8))) __bf16, b), c,
+        0, 0, 0);
+  }
+  __device__ static float4_t k16(short4_t a, short4_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<f16_t> {
+  __device__ static float4_t k32(short8_t a, short8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0,
+        0, 0);
+  }
+  __device__ static float4_t k16(short4_t a, short4_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(
+        __builtin_bit_cast(half4_t, a), __builtin_bit_cast(half4_t, b), c, 0,
+        0, 0);
+  }
+};
+
+// Byte permute (v_perm_b32): result byte i = byte sel_i of {hi:lo}.
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// Low 16 bits of a and b -> (a.lo | b.lo << 16).
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return perm_b32(b, a, 0x05040100u);
+}
+// High 16 bits of a and b -> (a.hi | b.hi << 16).
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return perm_b32(b, a, 0x07060302u);
+}
+
+}  // namespace mvllm

@@ -1,0 +1,186 @@
+"""Build one step's flattened model input and attention metadata on the GPU.
+
+Replaces the reference ModelRunner's packing (model_runner.py:724-900:
+``_build_model_input``, ``_flatten_model_input``, ``_build_slot_mapping``,
+``_build_block_table``; attention.py:56-85 ``build_metadata``) and, when
+capacities are given, the graph-padding copy (model_runner.py:78-122,
+``_CudaGraphExecution.copy_input``).
+
+The host side only concatenates what the plan already holds into one int32
+payload (per-request counts, block ids, token ids) and sends it with one
+host-to-device copy; positions, query starts, context lengths, context
+starts, slot mapping, the null-padded block table and the sampling rows are
+then produced by two HIP launches per cache group (``mvllm_pack_batch``).
+No device value is read back.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from dataclasses import dataclass
+from itertools import chain
+
+import numpy as np
+import torch
+
+from micro_vllm_amd import _native
+from micro_vllm_amd.attention.attention import AttentionMetadata
+from micro_vllm_amd.attention.spec import AttentionSpec
+from micro_vllm_amd.worker.scheduler_output import SchedulerOutput
+
+
+@dataclass(frozen=True, slots=True, eq=False)
+class PackedBatch:
+    """Flattened tensors of one step (the reference's ``ModelInput``,
+    model_runner.py:51-60) with one metadata object per cache group."""
+
+    input_ids: torch.Tensor
+    positions: torch.Tensor
+    group_metadata: tuple[AttentionMetadata, ...]
+    request_ids: tuple[str, ...]
+    sampling_row_indices: torch.Tensor
+
+
+def pack_scheduler_output(
+    plan: SchedulerOutput,
+    *,
+    specs: Sequence[AttentionSpec],
+    block_size: int,
+    null_block_id: int,
+    device: torch.device | str,
+    token_capacity: int | None = None,
+    request_capacity: int | None = None,
+    block_table_width: int | None = None,
+) -> PackedBatch:
+    """Pack ``plan`` for every cache group (``specs[g]`` is group g's spec).
+
+    Without capacities the outputs have the reference's unpadded shapes
+    (block table width = the longest block list of the group). With
+    capacities they are padded the way a captured graph expects.
+    """
+
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise RuntimeError("GPU packing requires a GPU device")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    requests = plan.scheduled_requests
+    num_groups = len(specs)
+    num_requests = len(requests)
+    for request in requests:
+        if len(request.block_tables) < num_groups:
+            raise ValueError(
+                f"request {request.request_id!r} has {len(request.block_tables)} block tables "
+                f"for {num_groups} cache groups"
+            )
+        if len(request.input_token_ids) != request.num_scheduled_tokens:
+            raise ValueError(
+                f"request {request.request_id!r} schedules {request.num_scheduled_tokens} "
+                f"tokens but carries {len(request.input_token_ids)} input ids"
+            )
+    scheduled = np.fromiter((r.num_scheduled_tokens for r in requests), dtype=np.int64, count=num_requests)
+    computed = np.fromiter((r.num_computed_tokens for r in requests), dtype=np.int64, count=num_requests)
+    sampling = np.fromiter((r.requires_sampling for r in requests), dtype=np.int64, count=num_requests)
+    num_tokens = int(scheduled.sum())
+    num_sampling = int(sampling.sum())
+    token_capacity = num_tokens if token_capacity is None else token_capacity
+    request_capacity = num_requests if request_capacity is None else request_capacity
+    if token_capacity < num_tokens or request_capacity < num_requests:
+        raise ValueError(
+            f"capacities ({token_capacity} tokens, {request_capacity} requests) are below the "
+            f"plan ({num_tokens}, {num_requests})"
+        )
+    if num_tokens + 1 > np.iinfo(np.int32).max:
+        raise ValueError("too many tokens for the int32 payload")
+
+    # Host payload: [token ids | per group: request info, block ids].
+    segments = [
+        np.fromiter(chain.from_iterable(r.input_token_ids for r in requests), dtype=np.int32, count=num_tokens)
+    ]
+    group_layout = []
+    widths = []
+    offset = num_tokens
+    for g in range(num_groups):
+        lengths = np.fromiter((len(r.block_tables[g].block_ids) for r in requests), dtype=np.int64, count=num_requests)
+        total_blocks = int(lengths.sum())
+        info = np.zeros((num_requests, _native.PACK_FIELDS), dtype=np.int32)
+        info[:, 0] = computed
+        info[:, 1] = scheduled
+        info[:, 2] = lengths
+        info[:, 3] = sampling
+        ids = np.fromiter(
+            chain.from_iterable(r.block_tables[g].block_ids for r in requests), dtype=np.int32, count=total_blocks
+        )
+        max_len = int(lengths.max()) if num_requests else 0
+        width = max_len if block_table_width is None else block_table_width
+        if width < max_len:
+            raise ValueError(f"block_table_width {width} is below the longest block list ({max_len})")
+        widths.append(width)
+        group_layout.append((offset, offset + info.size, total_blocks))
+        segments.extend((info.reshape(-1), ids))
+        offset += info.size + total_blocks
+    host = torch.from_numpy(np.concatenate(segments) if segments else np.zeros(0, np.int32))
+    if host.numel() == 0:
+        host = torch.zeros(1, dtype=torch.int32)
+    payload = host.pin_memory().to(device, non_blocking=True)
+
+    i64 = dict(dtype=torch.int64, device=device)
+    input_ids = torch.empty(token_capacity, **i64)
+    positions = torch.empty(token_capacity, **i64)
+    query_start_locations = torch.empty(request_capacity + 1, **i64)
+    context_lengths = torch.empty(request_capacity, **i64)
+    sampling_rows = torch.empty(num_sampling, **i64)
+    lib = _native.load()
+    stream = _native.stream_handle(device)
+    base = payload.data_ptr()
+    metadata = []
+    for g, spec in enumerate(specs):
+        info_offset, ids_offset, total_blocks = group_layout[g]
+        context_starts = torch.empty(token_capacity, **i64)
+        slot_mapping = torch.empty(token_capacity, **i64)
+        block_table = torch.empty((request_capacity, widths[g]), **i64)
+        kind, parameter = spec.kernel_code()
+        first = g == 0
+        args = _native.PackArgs()
+        args.request_info = base + 4 * info_offset if num_requests else None
+        args.block_ids = base + 4 * ids_offset if total_blocks else None
+        args.token_ids = base if num_tokens else None
+        args.num_requests = num_requests
+        args.num_tokens = num_tokens
+        args.num_block_ids = total_blocks
+        args.block_size = block_size
+        args.null_block_id = null_block_id
+        args.spec_kind = kind
+        args.spec_parameter = parameter
+        args.token_capacity = token_capacity
+        args.request_capacity = request_capacity
+        args.block_table_width = widths[g]
+        args.input_ids = input_ids.data_ptr() if first and token_capacity else None
+        args.positions = positions.data_ptr() if first and token_capacity else None
+        args.context_starts = context_starts.data_ptr() if token_capacity else None
+        args.query_start_locations = query_start_locations.data_ptr() if first else None
+        args.context_lengths = context_lengths.data_ptr() if first and request_capacity else None
+        args.block_table = block_table.data_ptr() if block_table.numel() else None
+        args.slot_mapping = slot_mapping.data_ptr() if token_capacity else None
+        args.sampling_rows = sampling_rows.data_ptr() if first and num_sampling else None
+        _native.check(lib.mvllm_pack_batch(args, stream), "mvllm_pack_batch")
+        metadata.append(
+            AttentionMetadata(
+                query_positions=positions,
+                query_context_start_positions=context_starts,
+                query_start_locations=query_start_locations,
+                context_lengths=context_lengths,
+                block_table=block_table,
+                slot_mapping=slot_mapping,
+                block_size=block_size,
+            )
+        )
+    # `payload` was allocated on the current stream, so the caching allocator
+    # reuses its memory only for work ordered after these launches.
+    return PackedBatch(
+        input_ids=input_ids,
+        positions=positions,
+        group_metadata=tuple(metadata),
+        request_ids=tuple(r.request_id for r in requests),
+        sampling_row_indices=sampling_rows,
+    )

@@ -1,0 +1,298 @@
+"""GPU parity of ragged paged attention against the oracle.
+
+The bar: the cache after the step is bit-exact with the oracle's write; the
+attention output is within max-abs 2e-2 / rtol 1e-2 (bf16) or 2e-3 / 2e-3
+(fp16) or 1e-5 (fp32) of the oracle's fp32 reference. Scenarios follow the
+reference's tests (test_triton_paged.py:119-292 with NaN-sentinel caches,
+graph padding and bounded specs; test_spike_triton_paged.py:215-319 ragged
+MHA/GQA/7:1/MQA/Qwen3 shapes) plus decode-kernel stress cases (contexts
+around split and block boundaries, every supported group size, sliding
+windows), the small mixed batch (contexts [17, 64, 130, 255]), a sampled
+check of the 256-sequence Qwen3 decode batch, and graph replay.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _golden import GOLDEN, batch_from_case, cache_from_case
+from _oracle_bridge import (
+    assert_attention_close,
+    assert_cache_bit_exact,
+    oracle_step,
+    subset_step,
+    to_oracle,
+)
+from micro_vllm_amd import workloads
+from micro_vllm_amd.attention import (
+    Attention,
+    AttentionMetadata,
+    ChunkedLocalSpec,
+    FullAttentionSpec,
+    SlidingWindowSpec,
+    map_cache_slots,
+)
+from micro_vllm_amd.attention.operators.registry import get_attention_operator_class
+
+pytestmark = pytest.mark.gpu
+
+TOL = {
+    torch.bfloat16: dict(atol=2e-2, rtol=1e-2),
+    torch.float16: dict(atol=2e-3, rtol=2e-3),
+    torch.float32: dict(atol=1e-5, rtol=1e-5),
+}
+
+
+def operator():
+    return get_attention_operator_class("mi355x_paged")()
+
+
+def run_and_check(query, key, value, cache, md, dtype):
+    before = cache.clone()
+    out = operator()(query, key, value, cache, md)
+    torch.cuda.synchronize()
+    expected_cache, expected = oracle_step(query, key, value, before, md)
+    assert out.shape == query.shape and out.dtype == query.dtype and out.device == query.device
+    assert_cache_bit_exact(cache, expected_cache)
+    assert_attention_close(out, expected, **TOL[dtype])
+    return out
+
+
+# ------------------------------------------------------------ golden cases
+
+
+@pytest.mark.parametrize("c", GOLDEN["attention_cases"], ids=lambda c: c["name"])
+def test_golden_attention_cases(device, c):
+    dtype = torch.float16 if c["dtype"] == "float16" else torch.float32
+    cache = torch.as_tensor(cache_from_case(c), dtype=dtype, device=device)
+    b = batch_from_case(c)
+    md = AttentionMetadata(
+        query_positions=torch.as_tensor(b.query_positions, device=device),
+        query_context_start_positions=torch.as_tensor(b.query_context_start_positions, device=device),
+        query_start_locations=torch.as_tensor(b.query_start_locations, device=device),
+        context_lengths=torch.as_tensor(b.context_lengths, device=device),
+        block_table=torch.as_tensor(b.block_table, device=device),
+        slot_mapping=torch.as_tensor(b.slot_mapping, device=device),
+        block_size=b.block_size,
+    )
+    t = lambda x: torch.tensor(x, dtype=dtype, device=device)  # noqa: E731
+    out = operator()(t(c["query"]), t(c["key"]), t(c["value"]), cache, md)
+    torch.cuda.synchronize()
+    expected = torch.tensor(c["expect_output"], dtype=torch.float64)
+    torch.testing.assert_close(out.double().cpu(), expected, atol=c["tolerance"], rtol=0)
+
+
+# ------------------------------- reference operator scenarios (NaN caches)
+
+BLOCK_SIZE = 3
+BLOCK_TABLE = (6, 1, 4)
+
+
+def _inputs(num_tokens, device, dtype, hq=4, hkv=2, d=16):
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn((num_tokens, hq, d), generator=gen, device=device).to(dtype)
+    k = torch.randn((num_tokens, hkv, d), generator=gen, device=device).to(dtype)
+    v = torch.randn((num_tokens, hkv, d), generator=gen, device=device).to(dtype)
+    cache = torch.full((2, 7, BLOCK_SIZE, hkv, d), float("nan"), dtype=dtype, device=device)
+    return q, k, v, cache
+
+
+def _run_chunks(attention, q, k, v, cache, chunks, dtype):
+    table = torch.tensor((BLOCK_TABLE,), dtype=torch.int64, device=q.device)
+    outs = []
+    for start, end in chunks:
+        positions = torch.arange(start, end, dtype=torch.int64, device=q.device)
+        md = attention.build_metadata(
+            query_positions=positions,
+            query_start_locations=torch.tensor((0, end - start), device=q.device),
+            context_lengths=torch.tensor((end,), device=q.device),
+            block_table=table,
+            slot_mapping=map_cache_slots(positions, table[0], BLOCK_SIZE),
+            block_size=BLOCK_SIZE,
+        )
+        outs.append(run_and_check(q[start:end], k[start:end], v[start:end], cache, md, dtype))
+    return torch.cat(outs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("spec", [FullAttentionSpec(), SlidingWindowSpec(3), ChunkedLocalSpec(4)], ids=repr)
+@pytest.mark.parametrize("head_dim", [16, 128])
+def test_full_and_chunked_prefill_and_decode(device, dtype, spec, head_dim):
+    q, k, v, cache = _inputs(8, device, dtype, d=head_dim)
+    attention = Attention(spec, "mi355x_paged")
+    full_cache = cache.clone()
+    full = _run_chunks(attention, q, k, v, full_cache, ((0, 8),), dtype)
+    inc_cache = cache.clone()
+    incremental = _run_chunks(attention, q, k, v, inc_cache, ((0, 3), (3, 6), (6, 7), (7, 8)), dtype)
+    torch.testing.assert_close(incremental.float(), full.float(), **TOL[dtype])
+    torch.testing.assert_close(full_cache, inc_cache, atol=0, rtol=0, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [16, 128])
+def test_graph_padding_neither_writes_cache_nor_returns_garbage(device, dtype, head_dim):
+    q, k, v, cache = _inputs(4, device, dtype, d=head_dim)
+    md = AttentionMetadata(
+        query_positions=torch.tensor((0, 1, 2, 0), device=device),
+        query_context_start_positions=torch.zeros(4, dtype=torch.int64, device=device),
+        query_start_locations=torch.tensor((0, 3, 3), device=device),
+        context_lengths=torch.tensor((3, 0), device=device),
+        block_table=torch.tensor((BLOCK_TABLE, (0, 0, 0)), device=device),
+        slot_mapping=torch.tensor((18, 19, 20, -1), device=device),
+        block_size=BLOCK_SIZE,
+    )
+    out = run_and_check(q, k, v, cache, md, dtype)
+    assert torch.count_nonzero(out[3]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(
+    ("hq", "hkv", "d"),
+    [(4, 4, 8), (4, 2, 8), (7, 1, 8), (4, 1, 7), (16, 8, 128), (32, 8, 128), (16, 16, 128)],
+    ids=["mha", "gqa", "group7", "mqa-dim7", "qwen3", "llama3", "mha128"],
+)
+def test_ragged_multi_request_with_arbitrary_starts(device, dtype, hq, hkv, d):
+    gen = torch.Generator(device=device).manual_seed(0)
+    q = torch.randn((6, hq, d), generator=gen, device=device).to(dtype)
+    k = torch.randn((6, hkv, d), generator=gen, device=device).to(dtype)
+    v = torch.randn((6, hkv, d), generator=gen, device=device).to(dtype)
+    cache = torch.randn((2, 6, 2, hkv, d), generator=gen, device=device).to(dtype)
+    md = AttentionMetadata(
+        query_positions=torch.tensor((0, 1, 2, 3, 4, 2), device=device),
+        query_context_start_positions=torch.tensor((0, 0, 1, 1, 2, 0), device=device),
+        query_start_locations=torch.tensor((0, 5, 6), device=device),
+        context_lengths=torch.tensor((5, 3), device=device),
+        block_table=torch.tensor(((3, 1, 5), (4, 0, -1)), device=device),
+        slot_mapping=torch.tensor((6, 7, 2, 3, 10, 0), device=device),
+        block_size=2,
+    )
+    run_and_check(q, k, v, cache, md, dtype)
+
+
+# ------------------------------------------------------ decode kernel stress
+
+
+def build_case(device, dtype, lengths, qlens, hq, hkv, d, bs, spec=None, seed=0, nan_cache=True):
+    """Random sequences; history rows written at their slots, everything
+    else in the cache NaN (stale/unmapped slots must never be read)."""
+
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    blocks_needed = [-(-L // bs) for L in lengths]
+    pool = rng.permutation(sum(blocks_needed) + 3)
+    num_blocks = len(pool) + 1
+    tables, cursor = [], 0
+    for n in blocks_needed:
+        tables.append(pool[cursor : cursor + n].tolist())
+        cursor += n
+    fill = float("nan") if nan_cache else 0.0
+    cache = torch.full((2, num_blocks, bs, hkv, d), fill, dtype=dtype, device=device)
+    flat = cache.view(2, -1, hkv, d)
+    positions = []
+    for r, (L, ql) in enumerate(zip(lengths, qlens)):
+        hist = torch.arange(0, L - ql, device=device)
+        if hist.numel():
+            slots = map_cache_slots(hist, torch.tensor(tables[r], device=device), bs)
+            flat[0, slots] = torch.randn((hist.numel(), hkv, d), generator=gen, device=device).to(dtype)
+            flat[1, slots] = torch.randn((hist.numel(), hkv, d), generator=gen, device=device).to(dtype)
+        positions.append(list(range(L - ql, L)))
+    kind, param = (spec.kernel_code() if spec is not None else (oracle.FULL, 0))
+    b = oracle.make_batch(positions, tables, block_size=bs, null_block_id=num_blocks - 1, spec=(kind, param))
+    md = AttentionMetadata(
+        query_positions=torch.as_tensor(b.query_positions, device=device),
+        query_context_start_positions=torch.as_tensor(b.query_context_start_positions, device=device),
+        query_start_locations=torch.as_tensor(b.query_start_locations, device=device),
+        context_lengths=torch.as_tensor(b.context_lengths, device=device),
+        block_table=torch.as_tensor(b.block_table, device=device),
+        slot_mapping=torch.as_tensor(b.slot_mapping, device=device),
+        block_size=bs,
+    )
+    n = sum(qlens)
+    q = torch.randn((n, hq, d), generator=gen, device=device).to(dtype)
+    k = torch.randn((n, hkv, d), generator=gen, device=device).to(dtype)
+    v = torch.randn((n, hkv, d), generator=gen, device=device).to(dtype)
+    return q, k, v, cache, md
+
+
+DECODE_LENGTHS = [1, 2, 15, 16, 17, 63, 64, 65, 255, 256, 257, 1000, 3000, 5003]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("hq", "hkv"), [(8, 8), (16, 8), (32, 8), (16, 2), (16, 1), (64, 4)], ids=lambda x: str(x))
+def test_decode_kernel_group_sizes_and_context_boundaries(device, dtype, hq, hkv):
+    lengths = DECODE_LENGTHS
+    q, k, v, cache, md = build_case(device, dtype, lengths, [1] * len(lengths), hq, hkv, 128, 16, seed=hq + hkv)
+    run_and_check(q, k, v, cache, md, dtype)
+
+
+@pytest.mark.parametrize("bs", [1, 5, 8, 32, 64])
+def test_decode_kernel_other_block_sizes(device, bs):
+    lengths = [1, 7, 33, 200, 777]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, [1] * len(lengths), 16, 8, 128, bs, seed=bs)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
+@pytest.mark.parametrize("spec", [SlidingWindowSpec(1), SlidingWindowSpec(100), SlidingWindowSpec(300), ChunkedLocalSpec(256), ChunkedLocalSpec(48)], ids=repr)
+def test_decode_kernel_bounded_specs(device, spec):
+    lengths = [5, 99, 100, 101, 300, 301, 1024, 2500]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, [1] * len(lengths), 16, 8, 128, 16, spec=spec, seed=3)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_mixed_prefill_and_decode_batch(device, dtype):
+    lengths = [40, 700, 1, 64, 3000, 17, 129]
+    qlens = [40, 33, 1, 1, 1, 5, 1]
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, 32, 8, 128, 16, seed=11)
+    run_and_check(q, k, v, cache, md, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_mixed_batch(device, dtype):
+    """Contexts [17, 64, 130, 255]: one 17-token prefill and three decodes."""
+
+    w = workloads.small_mixed(device, dtype=dtype)
+    run_and_check(w.query, w.key, w.value, w.cache, w.metadata, dtype)
+
+
+def test_qwen3_decode_batch_sampled(device):
+    """The 256-sequence Qwen3 decode batch (contexts U[128, 4096], 70k-block
+    pool): 12 sampled requests against the oracle, no NaN anywhere."""
+
+    w = workloads.qwen3_decode(device)
+    out = operator()(w.query, w.key, w.value, w.cache, w.metadata)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    order = np.argsort(w.context_lengths)
+    sample = sorted(set(order[:4].tolist() + order[-4:].tolist() + order[120:124].tolist()))
+    expected, got = subset_step(w, sample, out)
+    assert_attention_close(got, expected, **TOL[torch.bfloat16])
+
+
+def test_graph_replay_matches_eager(device):
+    q, k, v, cache, md = build_case(device, torch.bfloat16, [300, 1, 2000, 45], [1, 1, 1, 20], 16, 8, 128, 16, seed=5, nan_cache=False)
+    op = operator()
+    eager_cache = cache.clone()
+    eager = op(q, k, v, eager_cache, md)
+    torch.cuda.synchronize()
+    graph_cache = cache.clone()
+    op(q, k, v, graph_cache, md)  # warm up outside the graph
+    graph_cache.copy_(cache)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = op(q, k, v, graph_cache, md)
+    for _ in range(3):
+        graph_cache.copy_(cache)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        assert torch.equal(graph_cache, eager_cache)
+        # Eager work between replays.
+        _ = (q.float() * 2).sum().item()

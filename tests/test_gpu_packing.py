@@ -1,0 +1,182 @@
+"""GPU packing parity (bit-exact) against the reference's literal vectors and
+the oracle packing, including per-group metadata, graph padding and
+randomised plans; plus GPU context starts."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _golden import GOLDEN, SPEC_KINDS, requests_from_case
+from micro_vllm_amd.attention import Attention, ChunkedLocalSpec, FullAttentionSpec, SlidingWindowSpec
+from micro_vllm_amd.attention.attention import context_starts
+from micro_vllm_amd.worker.packing import pack_scheduler_output
+from micro_vllm_amd.worker.scheduler_output import CacheGroupBlockTable, ScheduledRequest, SchedulerOutput
+
+pytestmark = pytest.mark.gpu
+
+SPEC_OBJECTS = {
+    "full": lambda p: FullAttentionSpec(),
+    "sliding_window": lambda p: SlidingWindowSpec(p),
+    "chunked_local": lambda p: ChunkedLocalSpec(p),
+}
+
+
+def plan_from(requests: list[oracle.Request]) -> SchedulerOutput:
+    return SchedulerOutput(
+        tuple(
+            ScheduledRequest(
+                request_id=r.request_id,
+                input_token_ids=r.input_token_ids,
+                num_computed_tokens=r.num_computed_tokens,
+                num_scheduled_tokens=r.num_scheduled_tokens,
+                requires_sampling=r.requires_sampling,
+                block_tables=tuple(CacheGroupBlockTable(g) for g in r.block_tables),
+            )
+            for r in requests
+        )
+    )
+
+
+def check_against_oracle(packed, requests, specs, *, block_size, null_block_id, capacities=None):
+    for g, spec in enumerate(specs):
+        expected = oracle.pack(requests, group=g, block_size=block_size, null_block_id=null_block_id, spec=spec.kernel_code())
+        if capacities:
+            expected = oracle.graph_pad(expected, null_block_id=null_block_id, **capacities)
+        md = packed.group_metadata[g]
+        got = {
+            "positions": md.query_positions,
+            "context_starts": md.query_context_start_positions,
+            "query_start_locations": md.query_start_locations,
+            "context_lengths": md.context_lengths,
+            "block_table": md.block_table,
+            "slot_mapping": md.slot_mapping,
+        }
+        if g == 0:
+            got["input_ids"] = packed.input_ids
+            got["sampling_row_indices"] = packed.sampling_row_indices
+        for name, tensor in got.items():
+            assert tensor.dtype == torch.int64, name
+            assert tensor.cpu().numpy().tolist() == expected[name].tolist(), (g, name)
+
+
+@pytest.mark.parametrize("c", GOLDEN["packing_cases"], ids=lambda c: c["name"])
+def test_packing_golden_vectors(device, c):
+    requests = requests_from_case(c)
+    specs = [SPEC_OBJECTS[g["spec"][0]](g["spec"][1]) for g in c.get("groups", [{"spec": ["full", 0]}])]
+    caps = None
+    kwargs = {}
+    if "graph" in c:
+        width = max(len(r.block_tables[0]) for r in requests)
+        caps = dict(token_capacity=c["graph"]["token_capacity"], request_capacity=c["graph"]["request_capacity"], block_table_width=width)
+        kwargs = caps
+    packed = pack_scheduler_output(
+        plan_from(requests), specs=specs, block_size=c["block_size"], null_block_id=c["null_block_id"], device=device, **kwargs
+    )
+    torch.cuda.synchronize()
+    check_against_oracle(packed, requests, specs, block_size=c["block_size"], null_block_id=c["null_block_id"], capacities=caps)
+    expect = c.get("expect", {})
+    md = packed.group_metadata[0]
+    if "slot_mapping" in expect:
+        assert md.slot_mapping.tolist() == expect["slot_mapping"]
+    if "block_table" in expect:
+        assert md.block_table.tolist() == expect["block_table"]
+    if "query_start_locations" in expect:
+        assert md.query_start_locations.tolist() == expect["query_start_locations"]
+    if "input_ids" in expect:
+        assert packed.input_ids.tolist() == expect["input_ids"]
+    if "last_slot" in expect:
+        assert md.slot_mapping[-1].item() == expect["last_slot"]
+    if "block_table_shape" in expect:
+        assert list(md.block_table.shape) == expect["block_table_shape"]
+    for g, eg in enumerate(c.get("expect_groups", [])):
+        m = packed.group_metadata[g]
+        if "context_starts" in eg:
+            assert m.query_context_start_positions.tolist() == eg["context_starts"]
+        assert m.block_table.tolist() == eg["block_table"]
+        assert m.slot_mapping.tolist() == eg["slot_mapping"]
+    if len(packed.group_metadata) > 1:
+        assert packed.group_metadata[1].query_positions is packed.group_metadata[0].query_positions
+        assert packed.group_metadata[1].query_start_locations is packed.group_metadata[0].query_start_locations
+
+
+def random_requests(rng, num_requests, num_groups, block_size):
+    requests = []
+    for i in range(num_requests):
+        computed = int(rng.integers(0, 3000))
+        scheduled = int(rng.choice([1, 1, 1, int(rng.integers(1, 600))]))
+        total = computed + scheduled
+        tables = []
+        for _ in range(num_groups):
+            n = -(-total // block_size) + int(rng.integers(0, 3))  # some requests hold extra blocks
+            tables.append(tuple(int(x) for x in rng.integers(0, 100_000, n)))
+        requests.append(
+            oracle.Request(
+                request_id=f"r{i}",
+                input_token_ids=tuple(int(x) for x in rng.integers(0, 151_936, scheduled)),
+                num_computed_tokens=computed,
+                num_scheduled_tokens=scheduled,
+                requires_sampling=bool(rng.integers(0, 2)),
+                block_tables=tuple(tables),
+            )
+        )
+    return requests
+
+
+@pytest.mark.parametrize("num_requests", [0, 1, 7, 256, 1500])
+@pytest.mark.parametrize("padded", [False, True])
+def test_random_plans_match_oracle(device, num_requests, padded):
+    rng = np.random.default_rng(num_requests + 7 * padded)
+    block_size = 16
+    specs = [FullAttentionSpec(), SlidingWindowSpec(int(rng.integers(1, 500))), ChunkedLocalSpec(int(rng.integers(1, 500)))]
+    requests = random_requests(rng, num_requests, len(specs), block_size)
+    kwargs, caps = {}, None
+    if padded:
+        tokens = sum(r.num_scheduled_tokens for r in requests)
+        width = max((len(t) for r in requests for t in r.block_tables), default=0) + 5
+        caps = dict(token_capacity=tokens + 37, request_capacity=num_requests + 3, block_table_width=width)
+        kwargs = caps
+    packed = pack_scheduler_output(plan_from(requests), specs=specs, block_size=block_size, null_block_id=100_000, device=device, **kwargs)
+    torch.cuda.synchronize()
+    if not padded:
+        check_against_oracle(packed, requests, specs, block_size=block_size, null_block_id=100_000)
+        return
+    for g, spec in enumerate(specs):
+        expected = oracle.pack(requests, group=g, block_size=block_size, null_block_id=100_000, spec=spec.kernel_code())
+        expected = oracle.graph_pad(expected, null_block_id=100_000, **caps)
+        md = packed.group_metadata[g]
+        assert md.block_table.cpu().numpy().tolist() == expected["block_table"].tolist()
+        assert md.slot_mapping.cpu().numpy().tolist() == expected["slot_mapping"].tolist()
+        assert md.query_context_start_positions.cpu().numpy().tolist() == expected["context_starts"].tolist()
+        assert md.query_start_locations.cpu().numpy().tolist() == expected["query_start_locations"].tolist()
+        assert md.context_lengths.cpu().numpy().tolist() == expected["context_lengths"].tolist()
+        assert md.query_positions.cpu().numpy().tolist() == expected["positions"].tolist()
+    assert packed.input_ids.cpu().numpy().tolist() == expected["input_ids"].tolist()
+
+
+@pytest.mark.parametrize("c", GOLDEN["spec_cases"], ids=lambda c: f"{c['spec'][0]}-{c['spec'][1]}-{c['positions']}")
+def test_context_starts_golden_vectors(device, c):
+    spec = SPEC_OBJECTS[c["spec"][0]](c["spec"][1])
+    got = context_starts(torch.tensor(c["positions"], device=device), spec)
+    assert got.tolist() == c["expect"]
+
+
+def test_build_metadata_keeps_inputs_and_computes_starts(device):
+    positions = torch.tensor([2, 3, 4, 5], device=device)
+    args = dict(
+        query_positions=positions,
+        query_start_locations=torch.tensor([0, 4], device=device),
+        context_lengths=torch.tensor([6], device=device),
+        block_table=torch.tensor([[0, 1]], device=device),
+        slot_mapping=torch.tensor([2, 3, 4, 5], device=device),
+        block_size=4,
+    )
+    md = Attention(SlidingWindowSpec(3), "mi355x_paged").build_metadata(**args)
+    assert md.query_positions is positions
+    assert md.block_table is args["block_table"]
+    assert md.query_context_start_positions.tolist() == [0, 1, 2, 3]
+    big = torch.arange(0, 1_000_000, 7, device=device)
+    got = context_starts(big, ChunkedLocalSpec(13)).cpu().numpy()
+    assert np.array_equal(got, oracle.context_starts(oracle.CHUNKED_LOCAL, 13, big.cpu().numpy()))
