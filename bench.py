@@ -1,0 +1,299 @@
+"""Benchmark of the ragged paged-attention step on one MI355X.
+
+A step is one pass of the hot path over one synthetic batch: the
+``mi355x_paged`` operator's forward (KV-cache write + split-KV decode +
+combine; + MFMA prefill for multi-query requests). The default workload is
+the Qwen3-0.6B-head decode batch: 256 sequences, contexts U[128, 4096]
+(seed 0), 16 query / 8 KV heads, head_dim 128, block 16, bf16, blocks drawn
+from a shuffled 70,000-block pool, values N(0,1)*0.5.
+
+Reported (one JSON line on stdout):
+* ``value``: algorithmic HBM bytes of the step / step time, in GB/s;
+* ``roofline``: the decode kernel's algorithmic bytes per launch / its mean
+  duration measured with HIP events recorded around its launch, against
+  the 8 TB/s HBM peak;
+* ``cpu_baseline``: the numpy oracle (a restatement of the reference's
+  CPU attention) timed on this host, single-threaded, on a sample of the
+  same batch.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload qwen3_decode]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "micro-vllm_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "decode paged-attn HBM GB/s (% peak); e2e output tok/s, Qwen3-0.6B bf16"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+class HipEvents:
+    """hipEvent_t handles through the HIP runtime torch has loaded."""
+
+    def __init__(self):
+        import torch
+
+        lib_dir = Path(torch.__file__).resolve().parent / "lib"
+        candidates = [lib_dir / "libamdhip64.so", "libamdhip64.so.7", "libamdhip64.so"]
+        for name in candidates:
+            try:
+                self.hip = ctypes.CDLL(str(name))
+                break
+            except OSError:
+                continue
+        else:
+            raise RuntimeError("cannot locate the HIP runtime library")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, count: int) -> list[int]:
+        events = []
+        for _ in range(count):
+            handle = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(handle)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            events.append(handle.value)
+        return events
+
+    def elapsed_ms(self, start: int, stop: int) -> float:
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), ctypes.c_void_p(start), ctypes.c_void_p(stop)) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, events: list[int]) -> None:
+        for e in events:
+            self.hip.hipEventDestroy(ctypes.c_void_p(e))
+
+
+def decode_kernel_bytes(w) -> int:
+    """Algorithmic bytes one decode-kernel launch must move: every visible
+    K and V row once, Q read, O written, the block-table entries walked and
+    the per-request metadata."""
+
+    es = w.query.element_size()
+    rows = int(w.context_lengths.sum())
+    kv = rows * w.num_kv_heads * w.head_dim * 2 * es
+    n = int(w.query_lengths.sum())
+    qo = 2 * n * w.num_q_heads * w.head_dim * es
+    table = int(((w.context_lengths + w.block_size - 1) // w.block_size).sum()) * 8
+    meta = len(w.context_lengths) * 8 * 2 + 8 + n * 8 * 2
+    return kv + qo + table + meta
+
+
+def cpu_baseline(w, sample_requests: int, repeats: int) -> dict:
+    """Time the numpy oracle, single-threaded, on ``sample_requests``
+    sequences of the batch (their blocks copied into a compact host cache)."""
+
+    import numpy as np
+    import torch
+
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    order = np.arange(len(w.context_lengths))
+    step = max(1, len(order) // sample_requests)
+    chosen = order[::step][:sample_requests]
+    blocks = [w.block_lists[r] for r in chosen]
+    ids = np.concatenate(blocks)
+    compact = w.cache[:, torch.as_tensor(ids, device=w.cache.device)].cpu()
+    as_bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    cache = as_bits(compact)
+    cache = np.concatenate([cache, np.zeros_like(cache[:, :1])], axis=1)
+    tables, positions, cursor = [], [], 0
+    for r, b in zip(chosen, blocks):
+        tables.append(list(range(cursor, cursor + len(b))))
+        cursor += len(b)
+        L, q = int(w.context_lengths[r]), int(w.query_lengths[r])
+        positions.append(list(range(L - q, L)))
+    batch = oracle.make_batch(positions, tables, block_size=w.block_size, null_block_id=len(ids))
+    qsl = w.metadata.query_start_locations.cpu().numpy()
+    rows = np.concatenate([np.arange(qsl[r], qsl[r + 1]) for r in chosen])
+    rows_t = torch.as_tensor(rows, device=w.query.device)
+    q = as_bits(w.query[rows_t].cpu())
+    k = as_bits(w.key[rows_t].cpu())
+    v = as_bits(w.value[rows_t].cpu())
+
+    def run():
+        work = cache.copy()
+        start = time.perf_counter()
+        oracle.reference_forward(q, k, v, work, batch)
+        return time.perf_counter() - start
+
+    limiter = threadpool_limits(limits=1) if threadpool_limits else None
+    try:
+        run()
+        times = [run() for _ in range(repeats)]
+    finally:
+        if limiter is not None:
+            limiter.unregister()
+    seconds = statistics.median(times)
+    sample_bytes = _subset_bytes(w, chosen)
+    return {
+        "value": round(sample_bytes / seconds / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (
+            f"{len(chosen)} of {len(w.context_lengths)} sequences "
+            f"({int(w.context_lengths[chosen].sum())} context tokens), numpy oracle single-threaded, "
+            f"median of {repeats} runs: {seconds:.3f} s"
+        ),
+    }
+
+
+def _subset_bytes(w, chosen) -> int:
+    es = w.query.element_size()
+    L = w.context_lengths[chosen]
+    n = int(w.query_lengths[chosen].sum())
+    return int(L.sum()) * w.num_kv_heads * w.head_dim * 2 * es + 2 * n * w.num_q_heads * w.head_dim * es
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed"])
+    parser.add_argument("--cpu-sample", type=int, default=128, help="sequences timed by the CPU baseline")
+    parser.add_argument("--cpu-repeats", type=int, default=3)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on one GPU: --gpus {args.gpus} is not supported by this build "
+            "(the multi-GPU sharding of the path is described, not implemented).",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from micro_vllm_amd import _native, workloads
+    from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a visible GPU", file=sys.stderr)
+        return 1
+    _native.load()
+    device = torch.device("cuda", 0)
+    if args.workload == "qwen3_decode":
+        w = workloads.qwen3_decode(device)
+        description = (
+            "qwen3_decode: 256 decode sequences, contexts U[128,4096] seed 0, 16 q / 8 kv heads, "
+            "head_dim 128, block 16, bf16, 70k-block shuffled pool, values N(0,1)*0.5"
+        )
+    else:
+        w = workloads.llama3_mixed(device)
+        description = (
+            "llama3_mixed: 8 prefill chunks x 512 at offsets U[0,2048] + 248 decodes U[256,8192], "
+            "32 q / 8 kv heads, head_dim 128, block 16, bf16"
+        )
+    torch.cuda.synchronize()
+
+    hip = HipEvents()
+    steps = args.steps
+    marks = hip.create(2)
+    decode_events = hip.create(2 * steps)
+    prefill_events = hip.create(2 * steps)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+
+    def step(i: int | None):
+        timing = None
+        if i is not None:
+            timing = _native.Timing()
+            timing.decode_start, timing.decode_stop = decode_events[2 * i], decode_events[2 * i + 1]
+            timing.prefill_start, timing.prefill_stop = prefill_events[2 * i], prefill_events[2 * i + 1]
+        return hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata, timing=timing)
+
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    hip.hip.hipEventRecord(ctypes.c_void_p(marks[0]), ctypes.c_void_p(stream))
+    for i in range(steps):
+        step(i)
+    hip.hip.hipEventRecord(ctypes.c_void_p(marks[1]), ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    total_ms = hip.elapsed_ms(marks[0], marks[1])
+    ms_per_step = total_ms / steps
+    decode_ms = statistics.mean(hip.elapsed_ms(decode_events[2 * i], decode_events[2 * i + 1]) for i in range(steps))
+
+    step_bytes = workloads.decode_bytes(w)
+    kernel_bytes = decode_kernel_bytes(w)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = kernel_bytes / (decode_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": description,
+            "num_sequences": int(len(w.context_lengths)),
+            "num_tokens": int(w.query_lengths.sum()),
+            "context_tokens": int(w.context_lengths.sum()),
+            "step_bytes": int(step_bytes),
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "decode_split_kernel<bf16>",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel_us": round(decode_ms * 1e3, 2),
+            "kernel_bytes": int(kernel_bytes),
+        },
+    }
+    if args.workload == "llama3_mixed":
+        flops = workloads.prefill_flops(w)
+        try:
+            prefill_ms = statistics.mean(hip.elapsed_ms(prefill_events[2 * i], prefill_events[2 * i + 1]) for i in range(steps))
+            result["prefill"] = {
+                "flops": int(flops),
+                "kernel_us": round(prefill_ms * 1e3, 2),
+                "achieved_tflops": round(flops / (prefill_ms * 1e-3) / 1e12, 2),
+                "peak_tflops": BF16_PEAK_TFLOPS,
+            }
+        except RuntimeError:
+            result["prefill"] = {"flops": int(flops), "kernel_us": None, "note": "prefill ran on the generic kernel"}
+    hip.destroy(marks + decode_events + prefill_events)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_sample, args.cpu_repeats)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

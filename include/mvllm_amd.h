@@ -91,6 +91,9 @@ typedef struct mvllm_batch {
   int64_t block_table_width;
   int64_t block_table_stride[2];
   int64_t block_size;
+  int64_t max_query_len; /* largest query count of a request, if the caller
+                            knows it (<= 0: unknown). 1 lets a decode-only
+                            batch skip the prefill launch. */
 } mvllm_batch;
 
 /*
@@ -143,6 +146,32 @@ int mvllm_attention_forward(const mvllm_tensor3* query,
                             const mvllm_batch* batch, const mvllm_tensor3* out,
                             float scale, void* workspace,
                             int64_t workspace_bytes, void* stream);
+
+/*
+ * Optional kernel timing for measurement: hipEvent_t handles (as void*,
+ * NULL = not wanted) recorded on the launch stream immediately before and
+ * after the decode kernel and the prefill kernel (hipExtLaunchKernel).
+ */
+typedef struct mvllm_timing {
+  void* decode_start;
+  void* decode_stop;
+  void* prefill_start;
+  void* prefill_stop;
+} mvllm_timing;
+
+/*
+ * mvllm_attention_forward with per-kernel timing events. No counterpart in
+ * the reference: it exists so a benchmark can time the dominant kernel of
+ * a step on the stream it runs on.
+ */
+int mvllm_attention_forward_timed(const mvllm_tensor3* query,
+                                  const mvllm_tensor3* key,
+                                  const mvllm_tensor3* value,
+                                  const mvllm_kv_cache* cache,
+                                  const mvllm_batch* batch,
+                                  const mvllm_tensor3* out, float scale,
+                                  void* workspace, int64_t workspace_bytes,
+                                  const mvllm_timing* timing, void* stream);
 
 /*
  * Bit-exact gather of each request's visible K/V history into padded,
@@ -231,7 +260,7 @@ const char* mvllm_last_error(void);
 /* ABI version of this header (bumped on incompatible change). */
 int mvllm_abi_version(void);
 
-#define MVLLM_ABI_VERSION 1
+#define MVLLM_ABI_VERSION 2
 
 #ifdef __cplusplus
 }

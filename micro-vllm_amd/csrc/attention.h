@@ -61,9 +61,12 @@ __device__ __forceinline__ int64_t decode_num_splits(int64_t lo, int64_t hi, int
 }
 
 // Host-side launchers (one per kernel family).
+// Launchers; `start`/`stop` (may be null) bracket the main kernel's launch.
 int launch_generic(const AttnArgs& a, int32_t dtype, hipStream_t s);
-int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s);
-int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s);
+int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t start,
+                  hipEvent_t stop);
+int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t start,
+                   hipEvent_t stop);
 bool prefill_supported(const AttnArgs& a, int32_t dtype);
 
 // Device properties used for launch shapes (cached per device).

@@ -33,9 +33,9 @@ int32_t decode_split_tokens(int64_t num_requests, int64_t max_context) {
     const long v = std::strtol(env, nullptr, 10);
     if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) return static_cast<int32_t>(v);
   }
-  // Aim for roughly 8 (request, split) items per CU when every request
+  // Aim for roughly 4 (request, split) items per CU when every request
   // reaches half of the table's reach; never below 64 tokens per split.
-  const int64_t target_items = 8LL * device_cu_count();
+  const int64_t target_items = 4LL * device_cu_count();
   const int64_t est_tokens = num_requests * (max_context / 2 > 16 ? max_context / 2 : 16);
   int64_t split = (est_tokens + target_items - 1) / target_items;
   split = (split + 15) / 16 * 16;
@@ -106,11 +106,13 @@ extern "C" int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch, int
   return d.acc_bytes + d.ml_bytes;
 }
 
-extern "C" int mvllm_paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
-                                     const mvllm_batch* batch, const mvllm_tensor3* out,
-                                     float scale, void* workspace, int64_t workspace_bytes,
-                                     void* stream) {
-  clear_error();
+namespace mvllm {
+namespace {
+
+int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
+                    const mvllm_batch* batch, const mvllm_tensor3* out, float scale,
+                    void* workspace, int64_t workspace_bytes, const mvllm_timing* timing,
+                    void* stream) {
   if (int rc = check_tensor(query, "query")) return rc;
   if (int rc = check_tensor(out, "out")) return rc;
   if (!cache || !cache->data) return fail(MVLLM_ERR_INVALID, "cache is null");
@@ -179,10 +181,43 @@ extern "C" int mvllm_paged_attention(const mvllm_tensor3* query, const mvllm_kv_
   a.max_splits = d.max_splits;
   a.ws_acc = static_cast<float*>(workspace);
   a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + d.acc_bytes);
-  if (int rc = launch_decode(a, dtype, s)) return rc;
-  if (prefill_supported(a, dtype)) return launch_prefill(a, dtype, s);
+  hipEvent_t ds = timing ? static_cast<hipEvent_t>(timing->decode_start) : nullptr;
+  hipEvent_t de = timing ? static_cast<hipEvent_t>(timing->decode_stop) : nullptr;
+  hipEvent_t ps = timing ? static_cast<hipEvent_t>(timing->prefill_start) : nullptr;
+  hipEvent_t pe = timing ? static_cast<hipEvent_t>(timing->prefill_stop) : nullptr;
+  if (int rc = launch_decode(a, dtype, s, ds, de)) return rc;
+  // A batch known to hold only single-query requests needs no prefill launch.
+  if (batch->max_query_len == 1) return MVLLM_OK;
+  if (prefill_supported(a, dtype)) return launch_prefill(a, dtype, s, ps, pe);
   a.mode = 1;
   return launch_generic(a, dtype, s);
+}
+
+int attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,
+                      const mvllm_tensor3* value, const mvllm_kv_cache* cache,
+                      const mvllm_batch* batch, const mvllm_tensor3* out, float scale,
+                      void* workspace, int64_t workspace_bytes, const mvllm_timing* timing,
+                      void* stream) {
+  if (!batch) return fail(MVLLM_ERR_INVALID, "batch is null");
+  if (batch->num_tokens > 0) {
+    if (!batch->slot_mapping) return fail(MVLLM_ERR_INVALID, "slot_mapping is null");
+    if (int rc = mvllm_kv_write(key, value, cache, batch->slot_mapping, batch->num_tokens, stream))
+      return rc;
+  }
+  return paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, timing,
+                         stream);
+}
+
+}  // namespace
+}  // namespace mvllm
+
+extern "C" int mvllm_paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
+                                     const mvllm_batch* batch, const mvllm_tensor3* out,
+                                     float scale, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  clear_error();
+  return paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, nullptr,
+                         stream);
 }
 
 extern "C" int mvllm_attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,
@@ -191,11 +226,19 @@ extern "C" int mvllm_attention_forward(const mvllm_tensor3* query, const mvllm_t
                                        float scale, void* workspace, int64_t workspace_bytes,
                                        void* stream) {
   clear_error();
-  if (!batch) return fail(MVLLM_ERR_INVALID, "batch is null");
-  if (batch->num_tokens > 0) {
-    if (!batch->slot_mapping) return fail(MVLLM_ERR_INVALID, "slot_mapping is null");
-    if (int rc = mvllm_kv_write(key, value, cache, batch->slot_mapping, batch->num_tokens, stream))
-      return rc;
-  }
-  return mvllm_paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, stream);
+  return attention_forward(query, key, value, cache, batch, out, scale, workspace,
+                           workspace_bytes, nullptr, stream);
+}
+
+extern "C" int mvllm_attention_forward_timed(const mvllm_tensor3* query,
+                                             const mvllm_tensor3* key,
+                                             const mvllm_tensor3* value,
+                                             const mvllm_kv_cache* cache,
+                                             const mvllm_batch* batch, const mvllm_tensor3* out,
+                                             float scale, void* workspace,
+                                             int64_t workspace_bytes, const mvllm_timing* timing,
+                                             void* stream) {
+  clear_error();
+  return attention_forward(query, key, value, cache, batch, out, scale, workspace,
+                           workspace_bytes, timing, stream);
 }

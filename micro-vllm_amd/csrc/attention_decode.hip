@@ -22,6 +22,10 @@
 // Dao 2023; flash-decoding, Dao et al. 2023) and zero-fills tokens that
 // belong to no request.
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
+
+#include <hip/hip_ext.h>
 
 #include "attention.h"
 
@@ -38,7 +42,84 @@ __device__ __forceinline__ void split_hi_lo(float p, uint32_t& hi, uint32_t& lo)
   lo = Elem<T>::to_bits(p - Elem<T>::from_bits(hi));
 }
 
+// Epilogue shared by the decode kernels. acc[j][c][e] is
+// O[head hq][dim 64j + 16grp + 4e + c] (unnormalised), m / lt the running
+// max (exp2 domain) and the complete softmax denominator of this split. A
+// request with one split gets its output directly; otherwise the partial goes
+// to the workspace for the combine kernel.
 template <typename T>
+__device__ __forceinline__ void write_decode_result(const AttnArgs& a, int64_t r, int64_t qs, int hq,
+                                                    int split, int64_t ns, float m, float lt,
+                                                    const float4_t (&acc)[2][4], int grp) {
+  if (ns == 1) {
+    const float inv = 1.f / lt;
+    uint16_t* op = static_cast<uint16_t*>(a.out) + qs * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int i0 = 2 * i, i1 = 2 * i + 1;
+        w[i] = Elem<T>::to_bits(acc[j][i0 & 3][i0 >> 2] * inv) |
+               (Elem<T>::to_bits(acc[j][i1 & 3][i1 >> 2] * inv) << 16);
+      }
+      uint4* dst = reinterpret_cast<uint4*>(op + 64 * j + 16 * grp);
+      dst[0] = uint4{w[0], w[1], w[2], w[3]};
+      dst[1] = uint4{w[4], w[5], w[6], w[7]};
+    }
+    return;
+  }
+  const int64_t item = (r * a.max_splits + split) * a.num_q_heads + hq;
+  float* wp = a.ws_acc + item * kDim;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float4_t* dst = reinterpret_cast<float4_t*>(wp + 64 * j + 16 * grp);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      dst[e] = float4_t{acc[j][0][e], acc[j][1][e], acc[j][2][e], acc[j][3][e]};
+  }
+  if (grp == 0) a.ws_ml[item] = float2{m, lt};
+}
+
+// One 16-token tile of one KV head as MFMA A operands: lane (col, grp)
+// holds token `col`, dims 32i + 8grp .. +8 of K and of V.
+struct Tile {
+  short8_t k[4];
+  short8_t v[4];
+  bool ok;
+};
+
+template <bool NT>
+__device__ __forceinline__ short8_t load16(const uint16_t* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(reinterpret_cast<const short8_t*>(p));
+  } else {
+    return *reinterpret_cast<const short8_t*>(p);
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ void load_tile(const AttnArgs& a, const uint16_t* cache, int64_t r,
+                                          int64_t base, int64_t lo, int64_t end, int col,
+                                          int64_t head_off, Tile& t) {
+  const int64_t tk = base + col;
+  bool ok = tk >= lo && tk <= end;
+  int64_t off = 0;
+  if (ok) {
+    const int64_t b = block_of(a, r, tk);
+    ok = b >= 0;
+    off = b * a.c_s[1] + (tk % a.block_size) * a.c_s[2] + head_off;
+  }
+  const short8_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    t.k[i] = ok ? load16<NT>(cache + off + 32 * i) : zero;
+    t.v[i] = ok ? load16<NT>(cache + a.c_s[0] + off + 32 * i) : zero;
+  }
+  t.ok = ok;
+}
+
+template <typename T, bool PREFETCH, bool NT>
 __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[kMaxWaves][16 * kRow];
   const int wave = threadIdx.x >> 6;
@@ -83,27 +164,18 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
   const uint16_t* cache = static_cast<const uint16_t*>(a.cache);
   const int64_t head_off = static_cast<int64_t>(h) * kDim + 8 * grp;
 
+  Tile cur;
+  load_tile<NT>(a, cache, r, begin, lo, end, col, head_off, cur);
   for (int64_t base = begin; base <= end; base += 16) {
-    // This lane loads token `col` of the tile (A operand row), dims 32i + 8grp.
-    const int64_t tk = base + col;
-    bool ok = tk >= lo && tk <= end;
-    int64_t off = 0;
-    if (ok) {
-      const int64_t b = block_of(a, r, tk);
-      ok = b >= 0;
-      off = b * a.c_s[1] + (tk % a.block_size) * a.c_s[2] + head_off;
+    Tile nxt;
+    if constexpr (PREFETCH) {
+      if (base + 16 <= end) load_tile<NT>(a, cache, r, base + 16, lo, end, col, head_off, nxt);
     }
-    short8_t kv[4], vv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kv[i] = ok ? *reinterpret_cast<const short8_t*>(cache + off + 32 * i) : short8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      vv[i] = ok ? *reinterpret_cast<const short8_t*>(cache + a.c_s[0] + off + 32 * i) : short8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-    const uint64_t okmask = __ballot(ok);  // bit j (j < 16): token j of the tile is visible
+    const uint64_t okmask = __ballot(cur.ok);  // bit j (j < 16): token j of the tile is visible
 
     float4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sc = Mfma<T>::k32(kv[i], qv[i], sc);
+    for (int i = 0; i < 4; ++i) sc = Mfma<T>::k32(cur.k[i], qv[i], sc);
 
     float s[4];
 #pragma unroll
@@ -137,7 +209,7 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
     wave_lds_sync();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<short8_t*>(slab + col * kRow + 32 * i + 8 * grp) = vv[i];
+      *reinterpret_cast<short8_t*>(slab + col * kRow + 32 * i + 8 * grp) = cur.v[i];
     wave_lds_sync();
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -157,53 +229,247 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
         acc[j][c] = Mfma<T>::k16(av[c], pb_lo, acc[j][c]);
       }
     }
+    if constexpr (PREFETCH) {
+      cur = nxt;
+    } else {
+      if (base + 16 <= end) load_tile<NT>(a, cache, r, base + 16, lo, end, col, head_off, cur);
+    }
   }
 
-  // acc[j][c][e] is O[head col][dim 64j + 16grp + 4e + c] (unnormalised).
   const float l2 = l + shfl_xor_f(l, 16);
   const float lt = l2 + shfl_xor_f(l2, 32);
   if (col >= G) return;
-  const int64_t ns = decode_num_splits(lo, hi, a.split_tokens);
-  if (ns == 1) {
-    const float inv = 1.f / lt;
-    uint16_t* op = static_cast<uint16_t*>(a.out) + qs * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      uint32_t w[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int i0 = 2 * i, i1 = 2 * i + 1;
-        w[i] = Elem<T>::to_bits(acc[j][i0 & 3][i0 >> 2] * inv) |
-               (Elem<T>::to_bits(acc[j][i1 & 3][i1 >> 2] * inv) << 16);
-      }
-      uint4* dst = reinterpret_cast<uint4*>(op + 64 * j + 16 * grp);
-      dst[0] = uint4{w[0], w[1], w[2], w[3]};
-      dst[1] = uint4{w[4], w[5], w[6], w[7]};
-    }
-    return;
-  }
-  const int64_t item = (r * a.max_splits + split) * a.num_q_heads + hq;
-  float* wp = a.ws_acc + item * kDim;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    float4_t* dst = reinterpret_cast<float4_t*>(wp + 64 * j + 16 * grp);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      dst[e] = float4_t{acc[j][0][e], acc[j][1][e], acc[j][2][e], acc[j][3][e]};
-  }
-  if (grp == 0) a.ws_ml[item] = float2{m, lt};
+  write_decode_result<T>(a, r, qs, hq, split, decode_num_splits(lo, hi, a.split_tokens), m, lt, acc, grp);
 }
 
-// Blocks [0, R): merge split partials of multi-split decode requests.
-// Blocks [R, R + ceil(N / kZeroTokens)): zero tokens outside every request.
+// ---------------------------------------------------------------------------
+// Pipelined variant for block sizes that are multiples of 16 (every 16-token
+// tile then lies in one block). K and V tiles go straight from HBM to LDS
+// (global_load_lds_dwordx4): each load instruction covers 4 tokens x 256 B,
+// i.e. whole 128-byte lines. Tile slot (token t, 16-byte chunk q) lives at
+// LDS chunk 16t + (q ^ swz(t)) with swz(t) = t ^ ((t & 4) << 1), which keeps
+// 8 consecutive lanes inside one line on the global side and makes both LDS
+// read patterns (K rows as MFMA A operands, V columns for V^T) free of bank
+// conflicts. STAGES tiles per wave are in flight; waits are explicit vmcnt
+// counts because the only vector-memory instructions in the loop are these
+// tile loads (the split's block ids are fetched once, up front).
+
+constexpr int kTileBytes = 16 * 256;  // one 16-token tile of one head, K or V
+
+__device__ __forceinline__ int tile_swizzle(int t) { return t ^ ((t & 4) << 1); }
+
+// s_waitcnt with vmcnt <= n (n < 64), other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+  // n is wave-uniform; 8 loads per tile in flight, at most 3 tiles ahead.
+  if (n >= 24) wait_vmcnt<24>();
+  else if (n >= 16) wait_vmcnt<16>();
+  else if (n >= 8) wait_vmcnt<8>();
+  else wait_vmcnt<0>();
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <typename T, int STAGES>
+__global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int waves = blockDim.x >> 6;
+  const int h = blockIdx.x * waves + wave;
+  const int split = blockIdx.y;
+  const int64_t r = blockIdx.z;
+  if (h >= a.num_kv_heads) return;
+  const int64_t qs = a.qsl[r];
+  if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
+  int64_t lo, hi;
+  visible_range(a, r, qs, qs, lo, hi);
+  if (hi < lo) return;
+  const int64_t base0 = lo & ~int64_t(15);
+  const int64_t begin = base0 + static_cast<int64_t>(split) * a.split_tokens;
+  if (begin > hi) return;
+  const int64_t end = (begin + a.split_tokens - 1 < hi) ? begin + a.split_tokens - 1 : hi;
+  const int ntiles = static_cast<int>((end - begin) / 16 + 1);  // <= 64 (split <= 1024)
+
+  // Block id and in-block row of tile `lane` of this split, fetched once
+  // (block ids are < 2^31; a 16-aligned tile never straddles a block).
+  int32_t my_block = -1, my_row = 0;
+  if (lane < ntiles) {
+    const int64_t p = begin + 16 * lane;
+    my_block = static_cast<int32_t>(block_of(a, r, p));
+    my_row = static_cast<int32_t>(p % a.block_size);
+  }
+
+  const int G = a.group;
+  const int hq = h * G + col;
+  short8_t qv[4];
+  {
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + qs * a.q_s0 +
+                         static_cast<int64_t>(col < G ? hq : 0) * a.q_s1 + 8 * grp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      qv[i] = (col < G) ? *reinterpret_cast<const short8_t*>(qp + 32 * i) : short8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  uint8_t* wave_lds = smem + static_cast<size_t>(wave) * STAGES * 2 * kTileBytes;
+  const uint32_t wave_lds_addr = lds_address(wave_lds);
+  const uint16_t* cache = static_cast<const uint16_t*>(a.cache);
+  const int64_t head_elems = static_cast<int64_t>(h) * kDim;
+
+  // Load-side mapping: instruction i, this lane -> token 4i + lane/16 of the
+  // tile, 16-byte chunk q (element offset from the tile's first row).
+  int64_t lane_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 4 * i + (lane >> 4);
+    const int q = (lane & 15) ^ tile_swizzle(t);
+    lane_off[i] = t * a.c_s[2] + 8 * q;
+  }
+
+  auto issue = [&](int tile, int stage) {
+    const int32_t blk = __builtin_amdgcn_readlane(my_block, tile);
+    const int32_t row = __builtin_amdgcn_readlane(my_row, tile);
+    const uint32_t kdst = wave_lds_addr + stage * 2 * kTileBytes;
+    const uint32_t vdst = kdst + kTileBytes;
+    // An invalid block id masks the whole tile: read a valid dummy line instead.
+    const uint16_t* tile_k = blk >= 0 ? cache + static_cast<int64_t>(blk) * a.c_s[1] +
+                                            static_cast<int64_t>(row) * a.c_s[2] + head_elems
+                                      : cache;
+    const int64_t plane = blk >= 0 ? a.c_s[0] : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t* src = blk >= 0 ? tile_k + lane_off[i] : cache;
+      lds_dma_load16(src, kdst + i * 1024);
+      lds_dma_load16(src + plane, vdst + i * 1024);
+    }
+  };
+
+  float4_t acc[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[j][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+
+  // The block ids and Q must be in registers before the first tile address.
+  __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < ntiles) issue(s, s);
+
+  for (int k = 0; k < ntiles; ++k) {
+    const int stage = k % STAGES;
+    const int ahead = k + STAGES - 1;
+    if (ahead < ntiles) {
+      // The stage being refilled was read two iterations ago; its LDS reads
+      // have completed (their results fed the MFMAs), so it may be overwritten.
+      issue(ahead, ahead % STAGES);
+    }
+    const int later = (ntiles - 1 - k) < (STAGES - 1) ? (ntiles - 1 - k) : (STAGES - 1);
+    wait_vmcnt_dyn(8 * later);
+    __builtin_amdgcn_wave_barrier();
+    compiler_fence();
+
+    const int64_t tb = begin + 16 * static_cast<int64_t>(k);
+    const int64_t blk = __builtin_amdgcn_readlane(my_block, k);
+    // Token j of the tile is visible iff its position is in [lo, end] and the block is valid.
+    uint32_t okmask = 0;
+    if (blk >= 0) {
+      const int64_t first_ok = lo > tb ? lo - tb : 0;
+      const int64_t last_ok = end - tb < 15 ? end - tb : 15;
+      okmask = (last_ok >= first_ok) ? ((0xFFFFu >> (15 - last_ok)) & (0xFFFFu << first_ok)) : 0u;
+    }
+    const uint8_t* kt = wave_lds + stage * 2 * kTileBytes;
+    const uint8_t* vt = kt + kTileBytes;
+
+    float4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const short8_t kk = *reinterpret_cast<const short8_t*>(
+          kt + 16 * (16 * col + ((4 * i + grp) ^ tile_swizzle(col))));
+      sc = Mfma<T>::k32(kk, qv[i], sc);
+    }
+    float s[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      s[e] = ((okmask >> (4 * grp + e)) & 1u) ? sc[e] * a.scale_log2 : -INFINITY;
+    float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    bm = fmaxf(bm, shfl_xor_f(bm, 16));
+    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    const float mn = fmaxf(m, bm);
+    const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
+    float p[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[e] = (s[e] == -INFINITY) ? 0.f : exp2f(s[e] - mn);
+    l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[j][c] *= alpha;
+    }
+    m = mn;
+
+    uint32_t ph[4], pl[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) split_hi_lo<T>(p[e], ph[e], pl[e]);
+    const short4_t pb_hi = __builtin_bit_cast(short4_t, uint2{ph[0] | (ph[1] << 16), ph[2] | (ph[3] << 16)});
+    const short4_t pb_lo = __builtin_bit_cast(short4_t, uint2{pl[0] | (pl[1] << 16), pl[2] | (pl[3] << 16)});
+    // Rows of masked tokens may hold stale or non-finite data: zero them in V.
+    const uint32_t mlo = ((okmask >> (4 * grp)) & 1u ? 0xFFFFu : 0u) | ((okmask >> (4 * grp + 1)) & 1u ? 0xFFFF0000u : 0u);
+    const uint32_t mhi = ((okmask >> (4 * grp + 2)) & 1u ? 0xFFFFu : 0u) | ((okmask >> (4 * grp + 3)) & 1u ? 0xFFFF0000u : 0u);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint2 rv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 4 * grp + e;
+        const int q = 8 * j + (col >> 1);
+        rv[e] = *reinterpret_cast<const uint2*>(vt + 16 * (16 * t + (q ^ tile_swizzle(t))) + 8 * (col & 1));
+      }
+      short4_t av[4];
+      av[0] = __builtin_bit_cast(short4_t, uint2{pack_lo16(rv[0].x, rv[1].x) & mlo, pack_lo16(rv[2].x, rv[3].x) & mhi});
+      av[1] = __builtin_bit_cast(short4_t, uint2{pack_hi16(rv[0].x, rv[1].x) & mlo, pack_hi16(rv[2].x, rv[3].x) & mhi});
+      av[2] = __builtin_bit_cast(short4_t, uint2{pack_lo16(rv[0].y, rv[1].y) & mlo, pack_lo16(rv[2].y, rv[3].y) & mhi});
+      av[3] = __builtin_bit_cast(short4_t, uint2{pack_hi16(rv[0].y, rv[1].y) & mlo, pack_hi16(rv[2].y, rv[3].y) & mhi});
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc[j][c] = Mfma<T>::k16(av[c], pb_hi, acc[j][c]);
+        acc[j][c] = Mfma<T>::k16(av[c], pb_lo, acc[j][c]);
+      }
+    }
+    // All LDS reads of this stage must retire before a later issue refills it.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    compiler_fence();
+  }
+
+  const float l2 = l + shfl_xor_f(l, 16);
+  const float lt = l2 + shfl_xor_f(l2, 32);
+  if (col >= G) return;
+  write_decode_result<T>(a, r, qs, hq, split, decode_num_splits(lo, hi, a.split_tokens), m, lt, acc, grp);
+}
+
+// Blocks [0, R * kCombineGroups): merge split partials of multi-split
+// decode requests, kCombineHeads query heads per block, 32 lanes per head
+// (4 dims each), in one pass with a running maximum.
+// Blocks after that: zero tokens outside every request, kZeroTokens each.
 constexpr int kZeroTokens = 16;
+constexpr int kCombineHeads = 8;
 
 template <typename T>
-__global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t head_groups) {
   const int64_t R = a.num_requests;
-  if (blockIdx.x >= R) {
+  const int64_t combine_blocks = R * head_groups;
+  if (static_cast<int64_t>(blockIdx.x) >= combine_blocks) {
     const int64_t first = a.qsl[0], last = a.qsl[R];
-    const int64_t t0 = (blockIdx.x - R) * kZeroTokens;
+    const int64_t t0 = (blockIdx.x - combine_blocks) * kZeroTokens;
     const int64_t row = static_cast<int64_t>(a.num_q_heads) * a.head_dim;
     for (int64_t t = t0; t < t0 + kZeroTokens && t < a.num_tokens; ++t) {
       if (t >= first && t < last) continue;
@@ -215,66 +481,133 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a) {
     }
     return;
   }
-  const int64_t r = blockIdx.x;
+  const int64_t r = blockIdx.x / head_groups;
+  const int hq = static_cast<int>(blockIdx.x % head_groups) * kCombineHeads + (threadIdx.x >> 5);
+  if (hq >= a.num_q_heads) return;
   const int64_t qs = a.qsl[r];
   if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
   int64_t lo, hi;
   visible_range(a, r, qs, qs, lo, hi);
   const int64_t ns = decode_num_splits(lo, hi, a.split_tokens);
   if (ns == 1) return;
-  uint16_t* op = static_cast<uint16_t*>(a.out) + qs * a.o_s0;
-  for (int idx = threadIdx.x; idx < a.num_q_heads * 16; idx += blockDim.x) {
-    const int hq = idx >> 4;
-    const int d0 = (idx & 15) * 8;
-    uint32_t w[4];
-    if (ns == 0) {
-      // Nothing visible: softmax over no keys is NaN in the reference.
-      const uint32_t nan_bits = Elem<T>::to_bits(NAN);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = nan_bits | (nan_bits << 16);
-    } else {
-      float mx = -INFINITY;
-      for (int64_t s = 0; s < ns; ++s)
-        mx = fmaxf(mx, a.ws_ml[(r * a.max_splits + s) * a.num_q_heads + hq].x);
-      float sum = 0.f;
-      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int64_t s = 0; s < ns; ++s) {
-        const int64_t item = (r * a.max_splits + s) * a.num_q_heads + hq;
-        const float2 ml = a.ws_ml[item];
-        const float wgt = (ml.x == -INFINITY) ? 0.f : exp2f(ml.x - mx);
-        sum += wgt * ml.y;
-        const float4_t* src = reinterpret_cast<const float4_t*>(a.ws_acc + item * kDim + d0);
-        const float4_t v0 = src[0], v1 = src[1];
-        o[0] += wgt * v0[0]; o[1] += wgt * v0[1]; o[2] += wgt * v0[2]; o[3] += wgt * v0[3];
-        o[4] += wgt * v1[0]; o[5] += wgt * v1[1]; o[6] += wgt * v1[2]; o[7] += wgt * v1[3];
-      }
-      const float inv = 1.f / sum;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = Elem<T>::to_bits(o[2 * i] * inv) | (Elem<T>::to_bits(o[2 * i + 1] * inv) << 16);
+  const int d0 = (threadIdx.x & 31) * 4;
+  uint32_t w[2];
+  if (ns == 0) {
+    // Nothing visible: softmax over no keys is NaN in the reference.
+    const uint32_t nan_bits = Elem<T>::to_bits(NAN);
+    w[0] = w[1] = nan_bits | (nan_bits << 16);
+  } else {
+    float mx = -INFINITY, sum = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+    const int64_t first_item = r * a.max_splits * a.num_q_heads + hq;
+#pragma unroll 4
+    for (int64_t s = 0; s < ns; ++s) {
+      const int64_t item = first_item + s * a.num_q_heads;
+      const float2 ml = a.ws_ml[item];
+      const float4_t v = *reinterpret_cast<const float4_t*>(a.ws_acc + item * kDim + d0);
+      if (ml.x == -INFINITY) continue;
+      const float mn = fmaxf(mx, ml.x);
+      const float keep = exp2f(mx - mn);  // mx = -inf at the start: exp2(-inf) = 0
+      const float take = exp2f(ml.x - mn);
+      sum = sum * keep + take * ml.y;
+      o = o * keep + v * take;
+      mx = mn;
     }
-    *reinterpret_cast<uint4*>(op + static_cast<int64_t>(hq) * a.o_s1 + d0) = uint4{w[0], w[1], w[2], w[3]};
+    const float inv = 1.f / sum;
+    w[0] = Elem<T>::to_bits(o[0] * inv) | (Elem<T>::to_bits(o[1] * inv) << 16);
+    w[1] = Elem<T>::to_bits(o[2] * inv) | (Elem<T>::to_bits(o[3] * inv) << 16);
   }
+  uint16_t* op = static_cast<uint16_t*>(a.out) + qs * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1;
+  *reinterpret_cast<uint2*>(op + d0) = uint2{w[0], w[1]};
+}
+
+struct DecodeTuning {
+  bool lds_pipeline;  // the global->LDS pipelined kernel (block_size % 16 == 0)
+  int waves;          // waves (KV heads) per workgroup
+  int stages;         // tiles in flight per wave (pipelined kernel)
+  bool prefetch;      // register prefetch (general kernel)
+  bool nontemporal;   // non-temporal loads (general kernel)
+};
+
+DecodeTuning decode_tuning(const AttnArgs& a) {
+  DecodeTuning t;
+  t.lds_pipeline = a.block_size % 16 == 0 && a.split_tokens <= 1024;
+  t.waves = 4;
+  t.stages = 2;
+  t.prefetch = false;
+  t.nontemporal = false;
+  if (const char* env = std::getenv("MVLLM_DECODE_KERNEL")) {
+    if (std::strcmp(env, "general") == 0) t.lds_pipeline = false;
+  }
+  if (const char* env = std::getenv("MVLLM_DECODE_WAVES")) {
+    const int v = std::atoi(env);
+    if (v >= 1 && v <= kMaxWaves) t.waves = v;
+  }
+  if (const char* env = std::getenv("MVLLM_DECODE_STAGES")) {
+    const int v = std::atoi(env);
+    if (v >= 2 && v <= 4) t.stages = v;
+  }
+  if (const char* env = std::getenv("MVLLM_DECODE_PREFETCH")) t.prefetch = std::atoi(env) != 0;
+  if (const char* env = std::getenv("MVLLM_DECODE_NT")) t.nontemporal = std::atoi(env) != 0;
+  if (t.lds_pipeline && t.waves > 4) t.waves = 4;
+  if (t.waves > a.num_kv_heads) t.waves = a.num_kv_heads;
+  return t;
+}
+
+template <typename T, int STAGES>
+int launch_lds_kernel(const AttnArgs& a, dim3 grid, int waves, hipStream_t s, hipEvent_t start,
+                      hipEvent_t stop) {
+  const size_t lds = static_cast<size_t>(waves) * STAGES * 2 * kTileBytes;
+  if (lds > 64 * 1024) {
+    static bool raised = false;  // per instantiation; the attribute is process-wide
+    if (!raised) {
+      MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_split_lds_kernel<T, STAGES>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds)));
+      raised = true;
+    }
+  }
+  hipExtLaunchKernelGGL(decode_split_lds_kernel<T, STAGES>, grid, dim3(64 * waves), lds, s, start, stop,
+                        0, a);
+  MVLLM_LAUNCH_CHECK("decode_split_lds_kernel");
+  return MVLLM_OK;
 }
 
 template <typename T>
-int launch_decode_t(const AttnArgs& a, hipStream_t s) {
-  const int waves = a.num_kv_heads < kMaxWaves ? a.num_kv_heads : kMaxWaves;
+int launch_decode_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
+  const DecodeTuning tune = decode_tuning(a);
+  const int waves = tune.waves;
   const int groups = (a.num_kv_heads + waves - 1) / waves;
   if (a.max_splits > 65535 || a.num_requests > 65535)
     return fail(MVLLM_ERR_INVALID, "decode grid too large (%d splits, %lld requests)",
                 a.max_splits, (long long)a.num_requests);
   if (a.num_requests > 0) {
-    hipLaunchKernelGGL(decode_split_kernel<T>,
-                       dim3(groups, a.max_splits, static_cast<unsigned>(a.num_requests)),
-                       dim3(64 * waves), 0, s, a);
-    MVLLM_LAUNCH_CHECK("decode_split_kernel");
+    const dim3 grid(groups, a.max_splits, static_cast<unsigned>(a.num_requests));
+    const dim3 block(64 * waves);
+    if (tune.lds_pipeline) {
+      int rc = MVLLM_OK;
+      if (tune.stages == 2) rc = launch_lds_kernel<T, 2>(a, grid, waves, s, start, stop);
+      else if (tune.stages == 3) rc = launch_lds_kernel<T, 3>(a, grid, waves, s, start, stop);
+      else rc = launch_lds_kernel<T, 4>(a, grid, waves, s, start, stop);
+      if (rc) return rc;
+    } else {
+      if (tune.prefetch && tune.nontemporal)
+        hipExtLaunchKernelGGL(decode_split_kernel<T, true, true>, grid, block, 0, s, start, stop, 0, a);
+      else if (tune.prefetch)
+        hipExtLaunchKernelGGL(decode_split_kernel<T, true, false>, grid, block, 0, s, start, stop, 0, a);
+      else if (tune.nontemporal)
+        hipExtLaunchKernelGGL(decode_split_kernel<T, false, true>, grid, block, 0, s, start, stop, 0, a);
+      else
+        hipExtLaunchKernelGGL(decode_split_kernel<T, false, false>, grid, block, 0, s, start, stop, 0, a);
+      MVLLM_LAUNCH_CHECK("decode_split_kernel");
+    }
   }
-  const int64_t blocks = a.num_requests + (a.num_tokens + kZeroTokens - 1) / kZeroTokens;
+  const int32_t head_groups = (a.num_q_heads + kCombineHeads - 1) / kCombineHeads;
+  const int64_t blocks = a.num_requests * head_groups + (a.num_tokens + kZeroTokens - 1) / kZeroTokens;
   if (blocks > 0) {
     if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "combine grid too large");
-    hipLaunchKernelGGL(decode_combine_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256),
-                       0, s, a);
+    hipLaunchKernelGGL(decode_combine_kernel<T>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(32 * kCombineHeads), 0, s, a, head_groups);
     MVLLM_LAUNCH_CHECK("decode_combine_kernel");
   }
   return MVLLM_OK;
@@ -282,10 +615,11 @@ int launch_decode_t(const AttnArgs& a, hipStream_t s) {
 
 }  // namespace
 
-int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s) {
+int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t start,
+                  hipEvent_t stop) {
   if (a.head_dim != kDim) return fail(MVLLM_ERR_UNSUPPORTED, "decode kernel needs head_dim 128");
-  if (dtype == MVLLM_DTYPE_BF16) return launch_decode_t<bf16_t>(a, s);
-  if (dtype == MVLLM_DTYPE_F16) return launch_decode_t<f16_t>(a, s);
+  if (dtype == MVLLM_DTYPE_BF16) return launch_decode_t<bf16_t>(a, s, start, stop);
+  if (dtype == MVLLM_DTYPE_F16) return launch_decode_t<f16_t>(a, s, start, stop);
   return fail(MVLLM_ERR_UNSUPPORTED, "decode kernel needs bf16 or fp16");
 }
 

@@ -5,7 +5,7 @@ namespace mvllm {
 
 bool prefill_supported(const AttnArgs&, int32_t) { return false; }
 
-int launch_prefill(const AttnArgs&, int32_t, hipStream_t) {
+int launch_prefill(const AttnArgs&, int32_t, hipStream_t, hipEvent_t, hipEvent_t) {
   return fail(MVLLM_ERR_UNSUPPORTED, "prefill kernel not available");
 }
 

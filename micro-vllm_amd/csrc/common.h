@@ -74,12 +74,11 @@ __device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quiet).
+// fp32 -> bf16 bits, round to nearest even (the IEEE conversion the
+// hardware implements on gfx950); NaN stays NaN.
 __device__ __forceinline__ uint32_t float_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const __bf16 b = static_cast<__bf16>(f);
+  return __builtin_bit_cast(uint16_t, b);
 }
 
 __device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
@@ -138,6 +137,29 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
+
+// Direct HBM -> LDS load of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l's 16 bytes land at LDS byte address lds_base + 16 * l (lds_base is
+// wave-uniform). Issued through inline assembly so that the compiler does not
+// track the LDS write; callers order it with explicit s_waitcnt vmcnt counts.
+__device__ __forceinline__ void lds_dma_load16(const void* global_ptr, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(global_ptr), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+      : "memory", "m0");
+}
+
+// Byte address of an LDS location, for lds_dma_load16.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// Compiler-level fence: no memory access moves across it.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 // ---------------------------------------------------------------- MFMA ----
 //

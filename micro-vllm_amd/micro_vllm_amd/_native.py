@@ -16,7 +16,7 @@ import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libmvllm_amd.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_attention_workspace_bytes",
     "mvllm_paged_attention",
     "mvllm_attention_forward",
+    "mvllm_attention_forward_timed",
     "mvllm_gather_kv",
     "mvllm_context_starts",
     "mvllm_pack_batch",
@@ -92,6 +93,7 @@ class Batch(ctypes.Structure):
         ("block_table_width", _i64),
         ("block_table_stride", _i64 * 2),
         ("block_size", _i64),
+        ("max_query_len", _i64),
     ]
 
 
@@ -122,6 +124,15 @@ class PackArgs(ctypes.Structure):
     ]
 
 
+class Timing(ctypes.Structure):
+    _fields_ = [
+        ("decode_start", _ptr),
+        ("decode_stop", _ptr),
+        ("prefill_start", _ptr),
+        ("prefill_stop", _ptr),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing or unusable."""
 
@@ -145,6 +156,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_float, _ptr, _i64, _ptr,
     ]
     lib.mvllm_attention_forward.restype = ctypes.c_int
+    lib.mvllm_attention_forward_timed.argtypes = [
+        p(Tensor3), p(Tensor3), p(Tensor3), p(KVCache), p(Batch), p(Tensor3),
+        ctypes.c_float, _ptr, _i64, p(Timing), _ptr,
+    ]
+    lib.mvllm_attention_forward_timed.restype = ctypes.c_int
     lib.mvllm_gather_kv.argtypes = [p(KVCache), p(Batch), _i64, _ptr, _ptr, _ptr]
     lib.mvllm_gather_kv.restype = ctypes.c_int
     lib.mvllm_context_starts.argtypes = [_ptr, _i64, ctypes.c_int32, _i64, _ptr, _ptr]

@@ -27,6 +27,10 @@ class AttentionMetadata:
     block_table: torch.Tensor
     slot_mapping: torch.Tensor
     block_size: int
+    # Optional host-side hint (not in the reference's metadata): the largest
+    # number of queries of any request. Packing knows it without a device
+    # read; 1 lets a decode-only batch skip the prefill launch.
+    max_query_len: int | None = None
 
     @property
     def num_requests(self) -> int:

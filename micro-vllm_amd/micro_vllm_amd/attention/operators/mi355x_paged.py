@@ -68,6 +68,8 @@ def batch_descriptor(metadata: AttentionMetadata, device: torch.device) -> tuple
     b.block_table_stride[0] = table.stride(0)
     b.block_table_stride[1] = table.stride(1)
     b.block_size = metadata.block_size
+    hint = getattr(metadata, "max_query_len", None)
+    b.max_query_len = hint if hint is not None else -1
     return b, keep
 
 
@@ -135,8 +137,14 @@ def hip_paged_attention(
     value: torch.Tensor,
     layer_kv_cache: torch.Tensor,
     metadata: AttentionMetadata,
+    *,
+    timing: _native.Timing | None = None,
 ) -> torch.Tensor:
-    """Write current K/V, then ragged causal attention through the block table."""
+    """Write current K/V, then ragged causal attention through the block table.
+
+    ``timing`` (measurement only) carries hipEvent_t handles recorded around
+    the decode and prefill kernel launches.
+    """
 
     _check_inputs(query, key, value, layer_kv_cache, metadata)
     device = query.device
@@ -145,21 +153,23 @@ def hip_paged_attention(
     lib = _native.load()
     workspace_bytes = lib.mvllm_attention_workspace_bytes(batch, query.shape[1], query.shape[2])
     workspace = torch.empty(max(workspace_bytes, 1), dtype=torch.uint8, device=device)
-    _native.check(
-        lib.mvllm_attention_forward(
-            _native.tensor3(query),
-            _native.tensor3(key),
-            _native.tensor3(value),
-            _native.kv_cache(layer_kv_cache),
-            batch,
-            _native.tensor3(output),
-            1.0 / math.sqrt(query.shape[-1]),
-            workspace.data_ptr(),
-            workspace.numel(),
-            _native.stream_handle(device),
-        ),
-        "mvllm_attention_forward",
+    args = (
+        _native.tensor3(query),
+        _native.tensor3(key),
+        _native.tensor3(value),
+        _native.kv_cache(layer_kv_cache),
+        batch,
+        _native.tensor3(output),
+        1.0 / math.sqrt(query.shape[-1]),
+        workspace.data_ptr(),
+        workspace.numel(),
     )
+    stream = _native.stream_handle(device)
+    if timing is None:
+        status = lib.mvllm_attention_forward(*args, stream)
+    else:
+        status = lib.mvllm_attention_forward_timed(*args, timing, stream)
+    _native.check(status, "mvllm_attention_forward")
     del keep
     return output
 

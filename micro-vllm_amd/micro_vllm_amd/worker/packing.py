@@ -173,6 +173,7 @@ def pack_scheduler_output(
                 block_table=block_table,
                 slot_mapping=slot_mapping,
                 block_size=block_size,
+                max_query_len=int(scheduled.max()) if num_requests else 0,
             )
         )
     # `payload` was allocated on the current stream, so the caching allocator

@@ -137,6 +137,7 @@ def build(
         block_table=as_dev(table),
         slot_mapping=as_dev(slots),
         block_size=block_size,
+        max_query_len=int(query_lengths.max()) if len(query_lengths) else 0,
     )
     return Workload(
         name=name,

@@ -57,8 +57,9 @@ def test_struct_sizes_match_the_header_layout():
     # 8-byte pointer + 2 x int32 + int64 fields, no implicit padding.
     assert ctypes.sizeof(_native.Tensor3) == 8 + 8 + 6 * 8
     assert ctypes.sizeof(_native.KVCache) == 8 + 8 + 4 * 8 + 5 * 8
-    assert ctypes.sizeof(_native.Batch) == 6 * 8 + 3 * 8 + 2 * 8 + 8
+    assert ctypes.sizeof(_native.Batch) == 6 * 8 + 3 * 8 + 2 * 8 + 8 + 8
     assert ctypes.sizeof(_native.PackArgs) == 3 * 8 + 5 * 8 + 8 + 4 * 8 + 8 * 8
+    assert ctypes.sizeof(_native.Timing) == 4 * 8
 
 
 def test_library_rejects_bad_arguments_without_a_device():

@@ -296,3 +296,26 @@ def test_graph_replay_matches_eager(device):
         assert torch.equal(graph_cache, eager_cache)
         # Eager work between replays.
         _ = (q.float() * 2).sum().item()
+
+
+DECODE_VARIANTS = [
+    {"MVLLM_DECODE_KERNEL": "general"},
+    {"MVLLM_DECODE_KERNEL": "general", "MVLLM_DECODE_PREFETCH": "1", "MVLLM_DECODE_WAVES": "8"},
+    {"MVLLM_DECODE_STAGES": "2", "MVLLM_DECODE_WAVES": "4"},
+    {"MVLLM_DECODE_STAGES": "3", "MVLLM_DECODE_WAVES": "2"},
+    {"MVLLM_DECODE_STAGES": "4", "MVLLM_DECODE_WAVES": "1"},
+    {"MVLLM_DECODE_SPLIT": "64"},
+    {"MVLLM_DECODE_SPLIT": "1024"},
+]
+
+
+@pytest.mark.parametrize("env", DECODE_VARIANTS, ids=lambda e: ",".join(f"{k[13:]}={v}" for k, v in e.items()))
+@pytest.mark.parametrize("bs", [16, 32])
+def test_decode_tuning_variants_agree_with_oracle(device, monkeypatch, env, bs):
+    """Every decode kernel instantiation selectable by the launch tuning."""
+
+    for key, val in env.items():
+        monkeypatch.setenv(key, val)
+    lengths = DECODE_LENGTHS
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, [1] * len(lengths), 32, 8, 128, bs, seed=17)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
