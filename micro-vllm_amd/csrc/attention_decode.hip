@@ -258,13 +258,6 @@ constexpr int kTileBytes = 16 * 256;  // one 16-token tile of one head, K or V
 
 __device__ __forceinline__ int tile_swizzle(int t) { return t ^ ((t & 4) << 1); }
 
-// s_waitcnt with vmcnt <= n (n < 64), other counters unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 __device__ __forceinline__ void wait_vmcnt_dyn(int n) {
   // n is wave-uniform; 8 loads per tile in flight, at most 3 tiles ahead.
   if (n >= 24) wait_vmcnt<24>();

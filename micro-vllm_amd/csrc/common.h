@@ -152,6 +152,13 @@ __device__ __forceinline__ void lds_dma_load16(const void* global_ptr, uint32_t 
       : "memory", "m0");
 }
 
+// s_waitcnt with vmcnt <= N (N < 64), other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // Byte address of an LDS location, for lds_dma_load16.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(

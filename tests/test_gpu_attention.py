@@ -252,6 +252,131 @@ def test_mixed_prefill_and_decode_batch(device, dtype):
     run_and_check(q, k, v, cache, md, dtype)
 
 
+# ----------------------------------------------------- prefill kernel stress
+
+# Chunks of every alignment against the 16-token pages and 64-key tiles:
+# whole prompts, chunks after a history, single-page and multi-tile chunks,
+# chunks shorter than a workgroup's token block and ones spanning several.
+PREFILL_LENGTHS = [2, 17, 64, 700, 3000, 129, 600, 1100, 5000, 90]
+PREFILL_QLENS = [2, 17, 64, 33, 512, 100, 600, 77, 130, 3]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(
+    ("hq", "hkv"),
+    [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 2)],
+    ids=["g1", "g2-qwen3", "g4-llama3", "g8", "g16", "g16b"],
+)
+def test_prefill_kernel_group_sizes_and_chunk_offsets(device, dtype, hq, hkv):
+    q, k, v, cache, md = build_case(device, dtype, PREFILL_LENGTHS, PREFILL_QLENS, hq, hkv, 128, 16, seed=hq * 7 + hkv)
+    run_and_check(q, k, v, cache, md, dtype)
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_prefill_kernel_larger_blocks(device, bs):
+    lengths = [40, 700, 1, 300, 2049]
+    qlens = [40, 200, 1, 300, 65]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 32, 8, 128, bs, seed=bs)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
+@pytest.mark.parametrize(
+    "spec",
+    [SlidingWindowSpec(1), SlidingWindowSpec(37), SlidingWindowSpec(300), ChunkedLocalSpec(64), ChunkedLocalSpec(48), ChunkedLocalSpec(256)],
+    ids=repr,
+)
+@pytest.mark.parametrize(("hq", "hkv"), [(16, 8), (32, 8)], ids=["qwen3", "llama3"])
+def test_prefill_kernel_bounded_specs(device, spec, hq, hkv):
+    """Per-row windows: tiles cross every row's start, and keys before a
+    window (NaN in the cache here) must never reach the output."""
+
+    lengths = [300, 1000, 700, 129]
+    qlens = [300, 250, 512, 70]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, hq, hkv, 128, 16, spec=spec, seed=29)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
+def test_prefill_kernel_reloads_page_table_on_long_context(device):
+    """A 40,000-key visible range spans more than one LDS page-table load
+    (2,048 pages)."""
+
+    q, k, v, cache, md = build_case(device, torch.bfloat16, [40_000, 33], [48, 33], 16, 8, 128, 16, seed=41)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
+def test_prefill_kernel_unmapped_pages_are_masked(device):
+    """Block-table entries that are not valid block ids inside a visible
+    range are treated as masked keys (the decode kernel does the same)."""
+
+    dtype = torch.bfloat16
+    q, k, v, cache, md = build_case(device, dtype, [200, 150], [200, 40], 16, 8, 128, 16, seed=43, nan_cache=False)
+    table = md.block_table.clone()
+    table[0, 3] = -1                      # keys 48..63 of request 0
+    table[1, 1] = cache.shape[1] + 5      # keys 16..31 of request 1: out of range
+    slots = md.slot_mapping.clone()
+    req = torch.repeat_interleave(torch.arange(2, device=device), torch.tensor([200, 40], device=device))
+    logical = md.query_positions // 16
+    bad = ((req == 0) & (logical == 3)) | ((req == 1) & (logical == 1))
+    slots[bad] = -1
+    md2 = AttentionMetadata(
+        query_positions=md.query_positions,
+        query_context_start_positions=md.query_context_start_positions,
+        query_start_locations=md.query_start_locations,
+        context_lengths=md.context_lengths,
+        block_table=table,
+        slot_mapping=slots,
+        block_size=16,
+    )
+    before = cache.clone()
+    out = operator()(q, k, v, cache, md2)
+    torch.cuda.synchronize()
+    # Oracle: the same batch with the unmapped keys removed by a per-query
+    # visibility mask, computed densely in float64.
+    qf, kf, vf = q.double().cpu(), k.double().cpu(), v.double().cpu()
+    flat = before.double().cpu().view(2, -1, 8, 128)
+    tbl = md.block_table.cpu()
+    pos = md.query_positions.cpu()
+    lens = (200, 150)
+    qsl = (0, 200, 240)
+    expected = torch.zeros_like(qf)
+    for r in range(2):
+        L = lens[r]
+        keys_pos = torch.arange(L)
+        slot_ids = tbl[r, keys_pos // 16] * 16 + keys_pos % 16
+        kc = flat[0, slot_ids].clone()
+        vc = flat[1, slot_ids].clone()
+        # New tokens come from this step's K/V.
+        for t in range(qsl[r], qsl[r + 1]):
+            kc[pos[t]] = kf[t]
+            vc[pos[t]] = vf[t]
+        mapped = torch.ones(L, dtype=torch.bool)
+        mapped[(keys_pos // 16) == (3 if r == 0 else 1)] = False
+        kc[~mapped] = 0
+        vc[~mapped] = 0
+        for t in range(qsl[r], qsl[r + 1]):
+            for hq_ in range(16):
+                sc = (kc[:, hq_ // 2] @ qf[t, hq_]) / math.sqrt(128)
+                ok = mapped & (keys_pos <= pos[t])
+                sc[~ok] = -math.inf
+                expected[t, hq_] = torch.softmax(sc, 0) @ vc[:, hq_ // 2]
+    torch.testing.assert_close(out.double().cpu(), expected, **TOL[dtype])
+
+
+def test_llama3_mixed_batch_sampled(device):
+    """The Llama-3-head mixed batch (8 chunks of 512 at offsets U[0, 2048] +
+    248 decodes U[256, 8192]): every prefill chunk and a sample of decodes
+    against the oracle."""
+
+    w = workloads.llama3_mixed(device)
+    out = operator()(w.query, w.key, w.value, w.cache, w.metadata)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    chunks = [r for r in range(len(w.query_lengths)) if w.query_lengths[r] > 1]
+    sample = chunks + [8, 9, 100, 255]
+    expected, got = subset_step(w, sample, out)
+    assert_attention_close(got, expected, **TOL[torch.bfloat16])
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_small_mixed_batch(device, dtype):
     """Contexts [17, 64, 130, 255]: one 17-token prefill and three decodes."""
