@@ -175,6 +175,13 @@ def main() -> int:
     parser.add_argument("--cpu-sample", type=int, default=128, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument(
+        "--copy-calibration-mib",
+        type=int,
+        default=0,
+        help="after the timed steps, run one elementwise kernel that reads and writes this many MiB "
+        "(a plain copy of known traffic, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)",
+    )
     args = parser.parse_args()
 
     if args.gpus != 1:
@@ -287,6 +294,14 @@ def main() -> int:
         except RuntimeError:
             result["prefill"] = {"flops": int(flops), "kernel_us": None, "note": "prefill ran on the generic kernel"}
     hip.destroy(marks + decode_events + prefill_events)
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_sample, args.cpu_repeats)
     else:

@@ -7,26 +7,34 @@
 // all G query heads that share a KV head (GQA) read each K/V tile once.
 // Each wave owns 32 rows.
 //
-// Keys are processed in tiles of 64 (four 16-token pages). Every wave stages
-// one page of K and of V through registers into a double-buffered LDS tile
-// (one barrier per tile; the next page is in flight while the current tile
-// is computed). Per tile a wave computes
-//   S^T = K . Q^T      two v_mfma_f32_32x32x16 blocks (32 keys x 32 rows)
-// so each lane holds the scores of ONE row (lane % 32) for 16 keys per
-// block: the row max and sum are in-lane, plus one exchange with lane ^ 32.
-// P^T, as produced by the accumulator layout, is already the B operand of
-//   O^T += V^T . P^T   four 32x32x16 blocks per 16 keys (dims permuted)
-// and V^T comes from 8-byte LDS reads repacked with v_perm. The online
-// softmax (FlashAttention-2, Dao 2023) runs in the exp2 domain and rescales
-// the accumulators only when a row's maximum grows by more than 2^8
-// (lazy rescaling as in FlashAttention-3, Shah et al. 2024): the final
-// normalisation divides by a sum taken with the same offsets, so the result
-// is unchanged.
+// Keys are processed in tiles of 64 (four 16-token pages). Each wave moves
+// one page of K and of V per tile straight from HBM into LDS
+// (global_load_lds_dwordx4) into double-buffered K and V tiles: the loads of
+// tile k+1 are in flight while tile k is computed, with one barrier per tile.
+// The block ids of a tile's four pages are read from an LDS copy of the
+// block-table row one iteration ahead, so no table lookup sits on the
+// critical path. The K fragments of a tile are read in batches ahead of their
+// MFMAs, and the V operands of the first two 16-key steps are in flight
+// during the softmax.
 //
-// Masking is applied only on tiles that cross a row's visible range or hold
-// an unmapped page; there, keys outside every row's range of the wave are
-// also zeroed in V so that stale or non-finite cache rows cannot leak
-// through 0 * NaN.
+// Scores: S^T = K . Q^T as two v_mfma_f32_32x32x16 blocks (32 keys x 32
+// rows): each lane holds the scores of ONE row (lane % 32) for 16 keys per
+// block, so the row max and sum are in-lane plus one v_permlane32_swap.
+// P^T, as produced by the accumulator layout, is already the B operand of
+// O^T += V^T . P^T; the V^T A operand comes straight from transposing LDS
+// reads (ds_read_b64_tr_b16: in each 16-lane group, lane i receives element
+// i % 4 of the addresses given by lanes 4k + i / 4, k = 0..3).
+//
+// The online softmax (FlashAttention-2, Dao 2023) runs in the exp2 domain and
+// rescales the accumulators only when a row's maximum grows by more than 2^8
+// (lazy rescaling as in FlashAttention-3, Shah et al. 2024); the final
+// normalisation divides by a sum taken with the same offsets.
+//
+// Masking: scores are masked only on tiles that cross a row's visible range
+// or hold an unmapped page. V rows outside the workgroup's visible key range
+// (the tile overhang) and rows of unmapped pages are zeroed in LDS once per
+// tile, so stale or non-finite cache rows cannot leak through 0 * NaN and the
+// P.V path never branches.
 #include <climits>
 #include <cmath>
 
@@ -42,10 +50,9 @@ constexpr int kTileKeys = 64;
 constexpr int kWaves = 4;
 constexpr int kRows = kWaves * 32;                   // rows per workgroup
 constexpr int kTileBytes = kTileKeys * kDim * 2;     // one K (or V) tile: 16 KiB
-constexpr int kStageBytes = 2 * kTileBytes;          // K + V
 constexpr int kTablePages = 2048;                    // block ids held in LDS at a time
 constexpr int kChunkTiles = kTablePages / 4;
-constexpr size_t kLdsBytes = 2 * kStageBytes + kTablePages * 4 + 16 * 4;
+constexpr size_t kLdsBytes = 4 * kTileBytes + kTablePages * 4 + 16 * 4;  // K, V double buffers
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -95,18 +102,45 @@ __device__ __forceinline__ int32_t wave_max_i(int32_t v) {
 }
 
 // LDS byte offset of 16-byte chunk `chunk` of tile row `row` (256-byte rows).
-// XOR-swizzling the chunk with the row keeps both the 16-byte K reads (32
-// rows, one chunk) and the 8-byte V reads (one row, all chunks) free of bank
-// conflicts.
+// The chunk is XOR-swizzled with r ^ ((r & 2) << 2), r = row % 16. Both read
+// patterns are then free of bank conflicts: the K reads (32 rows, one chunk:
+// the swizzle is a bijection of r) and the transposing V reads (8 rows 8u ..
+// 8u + 7, chunks 4c .. 4c + 3: every physical chunk is hit exactly twice).
+__device__ __forceinline__ int tile_swizzle(int row) {
+  const int r = row & 15;
+  return r ^ ((r & 2) << 2);
+}
+
 __device__ __forceinline__ int tile_off(int row, int chunk) {
-  return row * 256 + ((chunk ^ (row & 15)) << 4);
+  return row * 256 + ((chunk ^ tile_swizzle(row)) << 4);
+}
+
+__device__ __forceinline__ float max_with_partner(float x) {
+  // v_permlane32_swap(x, x): lanes 0-31 get x[l + 32] in the second result,
+  // lanes 32-63 get x[l - 32] in the first; the other result is x itself.
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float sum_with_partner(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+// Transposing LDS read (see the file comment for its lane layout).
+__device__ __forceinline__ short4v lds_read_tr16(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(p));
 }
 
 template <typename T, bool PSPLIT>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_tok) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* const kv_lds = smem;
-  int32_t* const page_tbl = reinterpret_cast<int32_t*>(smem + 2 * kStageBytes);
+  uint8_t* const kbuf = smem;                   // K stages 0, 1 (16 KiB each)
+  uint8_t* const vbuf = smem + 2 * kTileBytes;  // V stages 0, 1
+  int32_t* const page_tbl = reinterpret_cast<int32_t*>(smem + 4 * kTileBytes);
   int32_t* const red = page_tbl + kTablePages;
 
   const int tid = threadIdx.x;
@@ -196,8 +230,30 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   const int32_t base = kmax >= kmin ? (kmin & ~15) : 0;
   const int32_t ntiles = kmax >= kmin ? (kmax - base) / kTileKeys + 1 : 0;
 
-  const uint32_t kv_addr = lds_address(kv_lds);
+  // Per-lane LDS byte offsets within a tile.
+  // K, A operand of S^T: row n (+ 32 bb), chunk 2 st + hh.
+  int koff[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) koff[st] = tile_off(n, 2 * st + hh);
+  // V, transposing reads for the A operand of O^T (dim block c, keys
+  // 8 hh + 4 u .. +4): lane (g = lane / 16, j = lane % 16) points at row
+  // 8 u + 4 (g / 2) + j / 4 (+ 32 bb + 16 s2), dims 32 c + 16 (g % 2) + 4 (j % 4).
+  int voff[8];
+  {
+    const int g = lane >> 4, jj = lane & 15;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int row = 8 * u + 4 * (g >> 1) + (jj >> 2);
+        const int dim = 32 * c + 16 * (g & 1) + 4 * (jj & 3);
+        voff[4 * u + c] = tile_off(row, dim >> 3) + 2 * (dim & 7);
+      }
+  }
+  const uint32_t kaddr = lds_address(kbuf);
+  const uint32_t vaddr = lds_address(vbuf);
   const uint32_t bs32 = static_cast<uint32_t>(a.block_size);
+
   for (int32_t c0 = 0; c0 < ntiles; c0 += kChunkTiles) {
     const int32_t nt = ntiles - c0 < kChunkTiles ? ntiles - c0 : kChunkTiles;
     // Block ids of the chunk's pages; pages past the last visible key are
@@ -208,183 +264,215 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     }
     __syncthreads();
 
-    // Wave w moves page w of tile tl (16 keys, K and V) straight into LDS
-    // stage `stage`: instruction i covers tile rows 16 w + 4 i .. +3; lane l
-    // lands at row 16 w + 4 i + l / 16, physical chunk l % 16, so it fetches
-    // the logical chunk that the swizzle puts there. An unmapped page is not
-    // loaded (its keys are masked and its V rows zeroed).
-    auto issue_page = [&](int32_t tl, int stage) {
-      const int32_t id = __builtin_amdgcn_readfirstlane(page_tbl[4 * tl + wave]);
-      if (id < 0) return;
+    // Wave w moves page w of tile tl into LDS: instruction i covers page rows
+    // 4 i .. 4 i + 3; lane l lands at row 4 i + l / 16, physical chunk l % 16,
+    // so it fetches the logical chunk that the swizzle puts there.
+    auto page_src = [&](int32_t tl, int32_t id) {
       const uint32_t pos = static_cast<uint32_t>(base + kTileKeys * (c0 + tl) + 16 * wave);
       const int64_t row0 = pos % bs32;
-      const uint16_t* page = cache + static_cast<int64_t>(id) * a.c_s[1] + row0 * a.c_s[2] + head_elems;
-      const uint32_t kdst = kv_addr + stage * kStageBytes + wave * 4096;
+      return cache + static_cast<int64_t>(id) * a.c_s[1] + row0 * a.c_s[2] + head_elems;
+    };
+    auto issue_k = [&](int32_t tl, int stage, int32_t id) {
+      if (id < 0) return;  // an unmapped page's keys are masked
+      const uint16_t* page = page_src(tl, id);
+      const uint32_t dst = kaddr + stage * kTileBytes + wave * 4096;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int rip = 4 * i + (lane >> 4);     // row in the page (its swizzle is rip)
-        const int chunk = (lane & 15) ^ rip;     // logical 16-byte chunk stored at lane's slot
-        const uint16_t* src = page + rip * a.c_s[2] + 8 * chunk;
-        lds_dma_load16(src, kdst + i * 1024);
-        lds_dma_load16(src + a.c_s[0], kdst + kTileBytes + i * 1024);
+        const int rip = 4 * i + (lane >> 4);
+        lds_dma_load16(page + rip * a.c_s[2] + 8 * ((lane & 15) ^ tile_swizzle(rip)), dst + i * 1024);
       }
     };
-
-    issue_page(0, 0);
-    wait_vmcnt<0>();
-    __syncthreads();
-
-    for (int32_t tl = 0; tl < nt; ++tl) {
+    auto issue_v = [&](int32_t tl, int stage, int32_t id) {
+      uint8_t* slot = vbuf + stage * kTileBytes + wave * 4096;
+      if (id < 0) {
+        // Unmapped (or beyond the last visible key): zero rows.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(slot + i * 1024 + 16 * lane) = uint4{0, 0, 0, 0};
+        return;
+      }
+      const uint16_t* page = page_src(tl, id) + a.c_s[0];
+      const uint32_t dst = vaddr + stage * kTileBytes + wave * 4096;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rip = 4 * i + (lane >> 4);
+        lds_dma_load16(page + rip * a.c_s[2] + 8 * ((lane & 15) ^ tile_swizzle(rip)), dst + i * 1024);
+      }
+    };
+    // After the loads landed: zero the V rows of this wave's page that lie
+    // outside [kmin, kmax] (they may hold stale or non-finite data).
+    auto fix_v = [&](int32_t tl, int stage) {
+      const int32_t pos0 = base + kTileKeys * (c0 + tl) + 16 * wave;
+      if (pos0 >= kmin && pos0 + 15 <= kmax) return;
+      uint8_t* slot = vbuf + stage * kTileBytes + wave * 4096;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int32_t p = pos0 + 4 * i + (lane >> 4);
+        if (p < kmin || p > kmax) *reinterpret_cast<uint4*>(slot + i * 1024 + 16 * lane) = uint4{0, 0, 0, 0};
+      }
+    };
+    // One tile: S = K . Q^T, softmax, O^T += V^T . P^T. LDS reads are issued
+    // in batches ahead of the MFMAs that consume them (sched_barrier keeps
+    // the compiler from sinking them next to their uses).
+    // The four block ids of a tile (one LDS read; tiles past the chunk read
+    // the last valid entry and are never used).
+    auto tile_ids = [&](int32_t tl) {
+      const int32_t t = tl < nt ? tl : nt - 1;
+      return *reinterpret_cast<const int4*>(page_tbl + 4 * t);
+    };
+    auto page_mask = [&](int4 ids) {
+      return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+          (ids.x >= 0 ? 1 : 0) | (ids.y >= 0 ? 2 : 0) | (ids.z >= 0 ? 4 : 0) | (ids.w >= 0 ? 8 : 0)));
+    };
+    auto own_id = [&](int4 ids) {
+      const int32_t v = wave == 0 ? ids.x : wave == 1 ? ids.y : wave == 2 ? ids.z : ids.w;
+      return __builtin_amdgcn_readfirstlane(v);
+    };
+    // cur_ids: tile tl; nxt_ids: tile tl + 1 (read one iteration ahead).
+    int4 cur_ids = tile_ids(0), nxt_ids = tile_ids(1);
+    auto step = [&](int32_t tl) {
       const int stage = tl & 1;
-      // The other stage was last read before the previous barrier.
-      if (tl + 1 < nt) issue_page(tl + 1, stage ^ 1);
+      if (tl + 1 < nt) {
+        const int32_t id = own_id(nxt_ids);
+        issue_k(tl + 1, stage ^ 1, id);
+        issue_v(tl + 1, stage ^ 1, id);
+      }
+      const int4 fut_ids = tile_ids(tl + 2);
       const int32_t k0 = base + kTileKeys * (c0 + tl);
-      if (k0 <= w_hi_max && k0 + kTileKeys - 1 >= w_lo_min) {
-        uint32_t pv = 0;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) pv |= (page_tbl[4 * tl + p] >= 0 ? 1u : 0u) << p;
-        pv = __builtin_amdgcn_readfirstlane(pv);
-        const bool edge = k0 < w_lo_max || k0 + kTileKeys - 1 > w_hi_min || pv != 0xFu;
-        const uint8_t* kt = kv_lds + stage * kStageBytes;
-        const uint8_t* vt = kt + kTileBytes;
+      const uint32_t pv = page_mask(cur_ids);
+      const bool edge = k0 < w_lo_max || k0 + kTileKeys - 1 > w_hi_min || pv != 0xFu;
+      const uint8_t* kt = kbuf + stage * kTileBytes;
+      const uint8_t* vt = vbuf + stage * kTileBytes;
 
-        float16v s[2];
+      short8_t kf[2][8];
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-          s[bb] = float16v{};
-          const int row = 32 * bb + n;
+      for (int st = 0; st < 8; ++st) kf[0][st] = *reinterpret_cast<const short8_t*>(kt + koff[st]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int st = 0; st < 8; ++st) {
-            const short8_t kk = *reinterpret_cast<const short8_t*>(kt + tile_off(row, 2 * st + hh));
-            s[bb] = Mma32<T>::mma(kk, qv[st], s[bb]);
-          }
-        }
-        // s[bb][i] = score of key 32 bb + 8 (i / 4) + 4 hh + i % 4 for row n.
-        if (edge) {
-          const int32_t rlo = lo_n - k0, rhi = hi_n - k0;
+      for (int st = 0; st < 8; ++st) kf[1][st] = *reinterpret_cast<const short8_t*>(kt + 8192 + koff[st]);
+      float16v s_cur[2];
+      s_cur[0] = float16v{};
+      s_cur[1] = float16v{};
 #pragma unroll
-          for (int bb = 0; bb < 2; ++bb)
+      for (int st = 0; st < 8; ++st) s_cur[0] = Mma32<T>::mma(kf[0][st], qv[st], s_cur[0]);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int kk = 32 * bb + 8 * (i >> 2) + 4 * hh + (i & 3);
-              const bool page_ok = (pv >> (2 * bb + (i >> 3))) & 1u;
-              const bool vis = page_ok && kk >= rlo && kk <= rhi;
-              s[bb][i] = vis ? s[bb][i] : -INFINITY;
-            }
-        }
-        float mx = -INFINITY;
+      for (int st = 0; st < 8; ++st) s_cur[1] = Mma32<T>::mma(kf[1][st], qv[st], s_cur[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      // V operands of the first two 16-key steps, in flight during the softmax.
+      short4v vf[4][8];
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) vf[q][x] = lds_read_tr16(vt + 256 * (16 * q) + voff[x]);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // s_cur[bb][i] = score of key 32 bb + 8 (i / 4) + 4 hh + i % 4, row n.
+      if (edge) {
+        // The empty asm keeps the compiler from if-converting the masking
+        // into every tile: interior tiles skip it entirely.
+        asm volatile("");
+        const int32_t rlo = lo_n - k0, rhi = hi_n - k0;
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[bb][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mx_c = mx * cs;
-        const bool grow = mx_c > m_c + 8.f;
-        if (__ballot(grow)) {
-          const float m_new = grow ? mx_c : m_c;
-          const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
-          l *= alpha;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
-          m_c = m_new;
-        }
-        const float m_use = m_c == -INFINITY ? 0.f : m_c;
-
-        // Keys of the tile that no row of this wave may see (edge tiles only).
-        const int32_t vlo = w_lo_min - k0, vhi = w_hi_max - k0;
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-          float p[16];
-#pragma unroll
           for (int i = 0; i < 16; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[bb][i], cs, -m_use));
-            l += p[i];
+            const int kk = 32 * bb + 8 * (i >> 2) + 4 * hh + (i & 3);
+            const bool page_ok = (pv >> (2 * bb + (i >> 3))) & 1u;
+            const bool vis = page_ok && kk >= rlo && kk <= rhi;
+            s_cur[bb][i] = vis ? s_cur[bb][i] : -INFINITY;
           }
+      }
+      float mx = -INFINITY;
 #pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2) {
-            // P^T B operand: keys 32 bb + 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
-            uint32_t ph[4], pl[4];
+      for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
-              if constexpr (PSPLIT) {
-                const float2v back = Mma32<T>::unpack2(ph[w]);
-                pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
-              }
-            }
-            const short8_t pb_hi = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
-            short8_t pb_lo = {};
-            if constexpr (PSPLIT) pb_lo = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[bb][i]);
+      mx = max_with_partner(mx);
+      const float mx_c = mx * cs;
+      const bool grow = mx_c > m_c + 8.f;
+      if (__ballot(grow)) {
+        const float m_new = grow ? mx_c : m_c;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
+        l *= alpha;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+        m_c = m_new;
+      }
+      const float m_use = m_c == -INFINITY ? 0.f : m_c;
 
-            // V rows of those keys, dims 4 n .. 4 n + 3.
-            uint2 rv[2][4];
+      short8_t pb[4], pbl[4];
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+      for (int bb = 0; bb < 2; ++bb) {
+        float p[16];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int key = 32 * bb + 16 * s2 + 8 * u + 4 * hh + e;
-                rv[u][e] = *reinterpret_cast<const uint2*>(vt + tile_off(key, n >> 1) + 8 * (n & 1));
-              }
-            if (edge) {
-              const bool page_ok = (pv >> (2 * bb + s2)) & 1u;
+        for (int i = 0; i < 16; ++i) {
+          p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[bb][i], cs, -m_use));
+          l += p[i];
+        }
 #pragma unroll
-              for (int u = 0; u < 2; ++u)
+        for (int s2 = 0; s2 < 2; ++s2) {
+          // P^T B operand: keys 32 bb + 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
+          uint32_t ph[4], pl[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const int key = 32 * bb + 16 * s2 + 8 * u + 4 * hh + e;
-                  const bool keep = page_ok && key >= vlo && key <= vhi;
-                  rv[u][e].x = keep ? rv[u][e].x : 0u;
-                  rv[u][e].y = keep ? rv[u][e].y : 0u;
-                }
-            }
-            // A operand of dim block c: row m <-> dim 4 m + c.
-            short8_t av[4];
-            {
-              uint32_t w0[4], w1[4], w2[4], w3[4];
-#pragma unroll
-              for (int w = 0; w < 4; ++w) {
-                const uint2 x0 = rv[w >> 1][2 * (w & 1)];
-                const uint2 x1 = rv[w >> 1][2 * (w & 1) + 1];
-                w0[w] = pack_lo16(x0.x, x1.x);
-                w1[w] = pack_hi16(x0.x, x1.x);
-                w2[w] = pack_lo16(x0.y, x1.y);
-                w3[w] = pack_hi16(x0.y, x1.y);
-              }
-              av[0] = __builtin_bit_cast(short8_t, uint4{w0[0], w0[1], w0[2], w0[3]});
-              av[1] = __builtin_bit_cast(short8_t, uint4{w1[0], w1[1], w1[2], w1[3]});
-              av[2] = __builtin_bit_cast(short8_t, uint4{w2[0], w2[1], w2[2], w2[3]});
-              av[3] = __builtin_bit_cast(short8_t, uint4{w3[0], w3[1], w3[2], w3[3]});
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              oacc[c] = Mma32<T>::mma(av[c], pb_hi, oacc[c]);
-              if constexpr (PSPLIT) oacc[c] = Mma32<T>::mma(av[c], pb_lo, oacc[c]);
+          for (int w = 0; w < 4; ++w) {
+            ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
+            if constexpr (PSPLIT) {
+              const float2v back = Mma32<T>::unpack2(ph[w]);
+              pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
             }
           }
+          pb[2 * bb + s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
+          if constexpr (PSPLIT) pbl[2 * bb + s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+      // O^T += V^T . P^T over the four 16-key steps q; the V operands of
+      // step q + 2 are read while step q multiplies.
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (q + 2 < 4) {
+#pragma unroll
+          for (int x = 0; x < 8; ++x) vf[q + 2][x] = lds_read_tr16(vt + 256 * (16 * (q + 2)) + voff[x]);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const short4v lo4 = vf[q][c], hi4 = vf[q][4 + c];
+          const short8_t av = short8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          oacc[c] = Mma32<T>::mma(av, pb[q], oacc[c]);
+          if constexpr (PSPLIT) oacc[c] = Mma32<T>::mma(av, pbl[q], oacc[c]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
       wait_vmcnt<0>();
+      if (tl + 1 < nt) fix_v(tl + 1, stage ^ 1);
       __syncthreads();
+      cur_ids = nxt_ids;
+      nxt_ids = fut_ids;
+    };
+
+    {
+      const int32_t id = own_id(cur_ids);
+      issue_k(0, 0, id);
+      issue_v(0, 0, id);
     }
+    wait_vmcnt<0>();
+    fix_v(0, 0);
+    __syncthreads();
+    for (int32_t tl = 0; tl < nt; ++tl) step(tl);
   }
 
-  const float lt = l + __shfl_xor(l, 32, 64);
+  const float lt = sum_with_partner(l);
   if (!row_ok) return;
-  // O^T block c, register 4 q + e of lane (n, hh): dim 32 q + 16 hh + 4 e + c.
+  // O^T block c, register 4 q + e of lane (n, hh): dim 32 c + 8 q + 4 hh + e.
   const float inv = nonempty ? 1.f / lt : NAN;  // an empty visible range is NaN, as in the reference
-  uint16_t* op = static_cast<uint16_t*>(a.out) + tok * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1 + 16 * hh;
+  uint16_t* op = static_cast<uint16_t*>(a.out) + tok * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1 + 4 * hh;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    uint32_t w[8];
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w[2 * e] = Mma32<T>::pack2(oacc[0][4 * q + e] * inv, oacc[1][4 * q + e] * inv);
-      w[2 * e + 1] = Mma32<T>::pack2(oacc[2][4 * q + e] * inv, oacc[3][4 * q + e] * inv);
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t w0 = Mma32<T>::pack2(oacc[c][4 * q] * inv, oacc[c][4 * q + 1] * inv);
+      const uint32_t w1 = Mma32<T>::pack2(oacc[c][4 * q + 2] * inv, oacc[c][4 * q + 3] * inv);
+      *reinterpret_cast<uint2*>(op + 32 * c + 8 * q) = uint2{w0, w1};
     }
-    uint4* dst = reinterpret_cast<uint4*>(op + 32 * q);
-    dst[0] = uint4{w[0], w[1], w[2], w[3]};
-    dst[1] = uint4{w[4], w[5], w[6], w[7]};
-  }
 }
 
 template <typename T, bool PSPLIT>
