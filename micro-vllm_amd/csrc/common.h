@@ -152,6 +152,19 @@ __device__ __forceinline__ void lds_dma_load16(const void* global_ptr, uint32_t 
       : "memory", "m0");
 }
 
+// lds_dma_load16 for data read exactly once (the decode kernel's K/V
+// stream): the non-temporal hint lets the lines leave the caches first
+// instead of displacing data that is reused.
+__device__ __forceinline__ void lds_dma_load16_stream(const void* global_ptr, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off nt"
+      :
+      : "v"(global_ptr), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+      : "memory", "m0");
+}
+
 // s_waitcnt with vmcnt <= N (N < 64), other counters unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
