@@ -95,6 +95,26 @@ def decode_kernel_bytes(w) -> int:
     return kv + qo + table + meta
 
 
+TRAFFIC_PROFILES = {
+    "qwen3_decode": ROOT / "profiles" / "decode_qwen3_256seq_traffic.md",
+    "llama3_mixed": ROOT / "profiles" / "decode_llama3_mixed_traffic.md",
+}
+
+
+def measured_traffic(workload: str) -> int | None:
+    """HBM bytes per decode-kernel launch on this workload, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it
+    reads for a plain elementwise kernel of known traffic); None if absent."""
+
+    path = TRAFFIC_PROFILES.get(workload)
+    if path is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def cpu_baseline(w, sample_requests: int, repeats: int) -> dict:
     """Time the numpy oracle, single-threaded, on ``sample_requests``
     sequences of the batch (their blocks copied into a compact host cache)."""
@@ -172,8 +192,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed"])
-    parser.add_argument("--cpu-sample", type=int, default=128, help="sequences timed by the CPU baseline")
-    parser.add_argument("--cpu-repeats", type=int, default=3)
+    parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
+    parser.add_argument("--cpu-repeats", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument(
         "--copy-calibration-mib",
@@ -270,13 +290,13 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "decode_split_kernel<bf16>",
+            "kernel": "decode_split_lds_kernel<bf16, 2>",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.workload),
             "kernel_us": round(decode_ms * 1e3, 2),
             "kernel_bytes": int(kernel_bytes),
         },
