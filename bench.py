@@ -186,12 +186,74 @@ def _subset_bytes(w, chosen) -> int:
     return int(L.sum()) * w.num_kv_heads * w.head_dim * 2 * es + 2 * n * w.num_q_heads * w.head_dim * es
 
 
+def run_e2e(args, device) -> dict:
+    """Greedy generation with a random-init Qwen3-0.6B-shaped model: output
+    tokens per second of synchronized engine steps."""
+
+    import numpy as np
+    import torch
+
+    from micro_vllm_amd.attention.operators.registry import get_attention_operator_class
+    from micro_vllm_amd.harness import DecoderConfig, DecoderModel, GenerationEngine, Request
+
+    cfg = DecoderConfig.qwen3_0_6b()
+    model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=0)
+    rng = np.random.default_rng(0)
+    lengths = rng.integers(64, 1025, size=args.e2e_requests)
+    prompts = [rng.integers(0, cfg.vocab_size, size=int(n)).tolist() for n in lengths]
+    block_size = 16
+    per_request = -(-(int(lengths.max()) + args.e2e_max_tokens) // block_size)
+    num_blocks = per_request * args.e2e_requests + 1
+
+    # Warm-up: a few short requests through a separate engine (kernel loading, allocator).
+    warm = GenerationEngine(model, num_blocks=4 * 8 + 1, max_num_batched_tokens=8192, max_num_seqs=256)
+    warm.generate([Request(f"w{i}", prompts[i][:64], max_tokens=4) for i in range(min(4, len(prompts)))])
+    del warm
+    torch.cuda.synchronize(device)
+
+    engine = GenerationEngine(model, num_blocks=num_blocks, max_num_batched_tokens=8192, max_num_seqs=256)
+    requests = [Request(f"r{i}", p, max_tokens=args.e2e_max_tokens) for i, p in enumerate(prompts)]
+    result = engine.generate(requests)
+    return {
+        "metric": METRIC,
+        "value": round(result.output_tokens_per_second, 2),
+        "unit": "output tok/s",
+        "n_gpus": 1,
+        "steps": result.steps,
+        "warmup": 1,
+        "ms_per_step": round(result.step_seconds / result.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (
+                f"qwen3_e2e: Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads of 128, qk-norm, "
+                f"MLP 3072, vocab 151936, tied embeddings), random init seed 0, bf16; {args.e2e_requests} "
+                f"requests with random prompts U[64,1024], {args.e2e_max_tokens} greedy tokens each, "
+                "max_num_batched_tokens 8192, max_num_seqs 256, block 16, eager"
+            ),
+            "parameters": model.parameter_count(),
+            "prompt_tokens": result.prompt_tokens,
+            "output_tokens": result.output_tokens,
+            "step_seconds": round(result.step_seconds, 4),
+            "preemptions": result.preemptions,
+            "parallelism": "single GPU",
+        },
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed"])
+    parser.add_argument("--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed", "qwen3_e2e"])
+    parser.add_argument("--e2e-requests", type=int, default=256, help="requests of the qwen3_e2e workload")
+    parser.add_argument("--e2e-max-tokens", type=int, default=256, help="greedy output tokens per request (qwen3_e2e)")
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -222,6 +284,9 @@ def main() -> int:
         return 1
     _native.load()
     device = torch.device("cuda", 0)
+    if args.workload == "qwen3_e2e":
+        print(json.dumps(run_e2e(args, device)), flush=True)
+        return 0
     if args.workload == "qwen3_decode":
         w = workloads.qwen3_decode(device)
         description = (

@@ -1,0 +1,257 @@
+"""A minimal token-budgeted generation loop around the decoder model.
+
+Scheduling follows the reference Scheduler's semantics (core/scheduler.py):
+* each step has a token budget (`max_num_batched_tokens`) and a sequence cap
+  (`max_num_seqs`);
+* running requests are scheduled first, in order, each for
+  min(pending tokens, remaining budget) tokens (:84-122), so long prompts are
+  prefilled in chunks;
+* when the block pool runs dry the newest running request is preempted: its
+  blocks are freed, it goes back to the waiting queue, and it later
+  recomputes its tokens (:100-113);
+* waiting requests are then admitted first-in first-out while budget and
+  sequence slots remain (:124-157);
+* a request samples when its scheduled tokens reach the end of its known
+  tokens; greedy decoding takes the first maximal logit (sampling/
+  sampler.py:45-46) and a request finishes after `max_tokens` outputs
+  (stop tokens are ignored).
+
+Blocks come from a pool whose last id is the null block that pads block
+tables (core/block.py:39; model_runner.py:243-245). The step's flattened
+input and attention metadata are built on the GPU
+(`worker.packing.pack_scheduler_output`); sampling runs on the device with
+one device-to-host copy of the sampled token ids per step.
+"""
+
+from __future__ import annotations
+
+import time
+from collections import deque
+from dataclasses import dataclass, field
+
+import torch
+
+from micro_vllm_amd.attention.spec import FullAttentionSpec
+from micro_vllm_amd.harness.model import DecoderModel
+from micro_vllm_amd.worker.packing import pack_scheduler_output
+from micro_vllm_amd.worker.scheduler_output import (
+    CacheGroupBlockTable,
+    ScheduledRequest,
+    SchedulerOutput,
+)
+
+
+@dataclass
+class Request:
+    request_id: str
+    prompt_token_ids: list[int]
+    max_tokens: int
+    output_token_ids: list[int] = field(default_factory=list)
+    num_computed_tokens: int = 0
+    block_ids: list[int] = field(default_factory=list)
+
+    @property
+    def all_token_ids(self) -> list[int]:
+        return self.prompt_token_ids + self.output_token_ids
+
+    @property
+    def num_known_tokens(self) -> int:
+        return len(self.prompt_token_ids) + len(self.output_token_ids)
+
+    @property
+    def finished(self) -> bool:
+        return len(self.output_token_ids) >= self.max_tokens
+
+
+@dataclass
+class GenerationResult:
+    outputs: dict[str, list[int]]
+    steps: int
+    step_seconds: float
+    output_tokens: int
+    prompt_tokens: int
+    preemptions: int
+
+    @property
+    def output_tokens_per_second(self) -> float:
+        return self.output_tokens / self.step_seconds if self.step_seconds > 0 else 0.0
+
+
+class GenerationEngine:
+    """Continuous batching over one decoder model and its paged KV caches."""
+
+    def __init__(
+        self,
+        model: DecoderModel,
+        *,
+        num_blocks: int,
+        block_size: int = 16,
+        max_num_batched_tokens: int = 8192,
+        max_num_seqs: int = 256,
+    ) -> None:
+        c = model.config
+        self.model = model
+        self.block_size = block_size
+        self.max_num_batched_tokens = max_num_batched_tokens
+        self.max_num_seqs = max_num_seqs
+        # Physical pool: ids [0, num_blocks - 1) are allocatable, the last id
+        # is the null block used to pad block tables.
+        self.num_blocks = num_blocks
+        self.null_block_id = num_blocks - 1
+        self.kv_caches = [
+            torch.empty(
+                (2, num_blocks, block_size, c.num_key_value_heads, c.head_dim),
+                dtype=model.dtype,
+                device=model.device,
+            )
+            for _ in range(c.num_hidden_layers)
+        ]
+        self._free_blocks = deque(range(num_blocks - 1))
+        self._waiting: deque[Request] = deque()
+        self._running: list[Request] = []
+        self._requests: dict[str, Request] = {}
+        self.preemptions = 0
+
+    # ------------------------------------------------------------ requests
+    def add_request(self, request: Request) -> None:
+        if request.request_id in self._requests:
+            raise ValueError(f"duplicate request id {request.request_id!r}")
+        if not request.prompt_token_ids:
+            raise ValueError("a request needs at least one prompt token")
+        self._requests[request.request_id] = request
+        self._waiting.append(request)
+
+    def has_unfinished_requests(self) -> bool:
+        return bool(self._waiting or self._running)
+
+    # ------------------------------------------------------------- blocks
+    def _ensure_blocks(self, request: Request, num_tokens: int) -> bool:
+        needed = -(-num_tokens // self.block_size) - len(request.block_ids)
+        if needed <= 0:
+            return True
+        if needed > len(self._free_blocks):
+            return False
+        request.block_ids.extend(self._free_blocks.popleft() for _ in range(needed))
+        return True
+
+    def _free(self, request: Request) -> None:
+        self._free_blocks.extend(request.block_ids)
+        request.block_ids = []
+
+    # ----------------------------------------------------------- schedule
+    def _scheduled(self, request: Request, num_tokens: int) -> ScheduledRequest:
+        start = request.num_computed_tokens
+        tokens = request.all_token_ids[start : start + num_tokens]
+        return ScheduledRequest(
+            request_id=request.request_id,
+            input_token_ids=tuple(tokens),
+            num_computed_tokens=start,
+            num_scheduled_tokens=num_tokens,
+            requires_sampling=start + num_tokens == request.num_known_tokens,
+            block_tables=(CacheGroupBlockTable(tuple(request.block_ids)),),
+        )
+
+    def schedule(self) -> SchedulerOutput:
+        budget = self.max_num_batched_tokens
+        scheduled: list[ScheduledRequest] = []
+        preempted: list[str] = []
+        exhausted = False
+        for request in list(self._running):
+            if request not in self._running:
+                continue  # preempted as a victim earlier in this loop
+            if budget == 0 or len(scheduled) == self.max_num_seqs:
+                break
+            n = min(request.num_known_tokens - request.num_computed_tokens, budget)
+            while not self._ensure_blocks(request, request.num_computed_tokens + n):
+                if self._running[-1] is request:
+                    break
+                victim = self._running.pop()
+                self._free(victim)
+                victim.num_computed_tokens = 0
+                self._waiting.append(victim)
+                preempted.append(victim.request_id)
+                self.preemptions += 1
+            else:
+                scheduled.append(self._scheduled(request, n))
+                budget -= n
+                continue
+            if not scheduled:
+                raise RuntimeError(f"request {request.request_id} cannot fit in the KV cache")
+            exhausted = True
+            break
+        while (
+            self._waiting
+            and not exhausted
+            and budget > 0
+            and len(self._running) < self.max_num_seqs
+        ):
+            request = self._waiting[0]
+            n = min(request.num_known_tokens, budget)
+            if not self._ensure_blocks(request, n):
+                if not scheduled:
+                    raise RuntimeError(f"request {request.request_id} cannot fit in the KV cache")
+                break
+            scheduled.append(self._scheduled(request, n))
+            budget -= n
+            self._waiting.popleft()
+            self._running.append(request)
+        return SchedulerOutput(tuple(scheduled), tuple(preempted))
+
+    def _update(self, plan: SchedulerOutput, sampled: list[int]) -> None:
+        samples = iter(sampled)
+        for item in plan.scheduled_requests:
+            request = self._requests[item.request_id]
+            request.num_computed_tokens += item.num_scheduled_tokens
+            if item.requires_sampling:
+                request.output_token_ids.append(next(samples))
+                if request.finished:
+                    self._running.remove(request)
+                    self._free(request)
+
+    # ---------------------------------------------------------------- step
+    @torch.inference_mode()
+    def execute(self, plan: SchedulerOutput) -> list[int]:
+        """One model step on the GPU; returns the greedy tokens of the
+        sampling requests, in plan order."""
+
+        packed = pack_scheduler_output(
+            plan,
+            specs=[FullAttentionSpec()],
+            block_size=self.block_size,
+            null_block_id=self.null_block_id,
+            device=self.model.device,
+        )
+        hidden = self.model.forward(packed.input_ids, packed.positions, self.kv_caches, packed.group_metadata[0])
+        rows = packed.sampling_row_indices
+        if rows.numel() == 0:
+            return []
+        logits = self.model.logits(hidden.index_select(0, rows))
+        return logits.argmax(dim=-1).tolist()
+
+    def generate(self, requests: list[Request]) -> GenerationResult:
+        """Run every request to completion; time the synchronized steps
+        (schedule + execute + update, as the reference benchmark times
+        Engine.step, benchmarks/benchmark_engine.py:312-315)."""
+
+        for request in requests:
+            self.add_request(request)
+        steps = 0
+        seconds = 0.0
+        device = self.model.device
+        torch.cuda.synchronize(device)
+        while self.has_unfinished_requests():
+            start = time.perf_counter()
+            plan = self.schedule()
+            sampled = self.execute(plan)
+            torch.cuda.synchronize(device)
+            self._update(plan, sampled)
+            seconds += time.perf_counter() - start
+            steps += 1
+        return GenerationResult(
+            outputs={r.request_id: list(r.output_token_ids) for r in requests},
+            steps=steps,
+            step_seconds=seconds,
+            output_tokens=sum(len(r.output_token_ids) for r in requests),
+            prompt_tokens=sum(len(r.prompt_token_ids) for r in requests),
+            preemptions=self.preemptions,
+        )

@@ -1,0 +1,102 @@
+"""End-to-end greedy decoding with the HIP operator against the torch
+restatement of the reference operator.
+
+A random-init Qwen3-shaped decoder (2 layers, 16/8 heads of 128, qk-norm)
+generates with the `mi355x_paged` operator under a small token budget, so
+prompts are prefilled in chunks and decode steps mix with prefill chunks.
+Every generated position is then re-derived teacher-forced with the
+reference-semantics operator on the same weights: the greedy token must be
+the same, except where the reference's two largest logits are within bf16
+noise of each other (a legitimate near-tie; the survey's rule for
+random-init models), and the logits of both operators must agree to bf16
+accuracy.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _torch_reference import TorchReferenceAttention
+from micro_vllm_amd.attention.operators.registry import get_attention_operator_class
+from micro_vllm_amd.attention.spec import FullAttentionSpec
+from micro_vllm_amd.harness import DecoderConfig, DecoderModel, GenerationEngine, Request
+from micro_vllm_amd.worker.packing import pack_scheduler_output
+from micro_vllm_amd.worker.scheduler_output import CacheGroupBlockTable, ScheduledRequest, SchedulerOutput
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 8192
+# Logits have std ~0.64 at this init and are produced in bf16 (one ulp is
+# ~0.016 at magnitude 2), so a top-2 gap below ~3 ulps is a near-tie that a
+# one-ulp difference in an attention output can flip.
+NEAR_TIE = 0.05
+LOGIT_ATOL = 0.15     # max |logit difference| between the two operators
+
+
+def make_requests(seed, count, lo, hi, max_tokens):
+    rng = np.random.default_rng(seed)
+    return [
+        Request(f"r{i}", rng.integers(0, VOCAB, size=int(rng.integers(lo, hi + 1))).tolist(), max_tokens)
+        for i in range(count)
+    ]
+
+
+@torch.inference_mode()
+def teacher_forced_logits(model, sequences, device):
+    """Logits of every position of each sequence (one prefill step)."""
+
+    plan_items, block, tables = [], 0, []
+    for i, seq in enumerate(sequences):
+        nb = -(-len(seq) // 16)
+        tables.append(tuple(range(block, block + nb)))
+        block += nb
+        plan_items.append(
+            ScheduledRequest(f"s{i}", tuple(seq), 0, len(seq), True, (CacheGroupBlockTable(tables[-1]),))
+        )
+    caches = [
+        torch.zeros((2, block + 1, 16, model.config.num_key_value_heads, 128), dtype=model.dtype, device=device)
+        for _ in range(model.config.num_hidden_layers)
+    ]
+    packed = pack_scheduler_output(
+        SchedulerOutput(tuple(plan_items)), specs=[FullAttentionSpec()], block_size=16, null_block_id=block, device=device
+    )
+    hidden = model.forward(packed.input_ids, packed.positions, caches, packed.group_metadata[0])
+    return model.logits(hidden).float()
+
+
+def test_greedy_decoding_matches_reference_attention(device):
+    cfg = DecoderConfig.qwen3_0_6b(num_hidden_layers=2, vocab_size=VOCAB)
+    hip_model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=3)
+    ref_model = DecoderModel(cfg, TorchReferenceAttention(), device=device, seed=3)
+    requests = make_requests(seed=1, count=8, lo=20, hi=200, max_tokens=12)
+    engine = GenerationEngine(hip_model, num_blocks=256, max_num_batched_tokens=160, max_num_seqs=6)
+    result = engine.generate(requests)
+    assert result.output_tokens == 8 * 12
+    assert result.steps > 12  # chunked prefill and mixed steps happened
+
+    sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in requests]
+    ref_logits = teacher_forced_logits(ref_model, sequences, device)
+    hip_logits = teacher_forced_logits(hip_model, sequences, device)
+    assert torch.isfinite(hip_logits).all()
+    max_diff = (hip_logits - ref_logits).abs().max().item()
+    print(f"max |logit difference| {max_diff:.4f}")
+    assert max_diff < LOGIT_ATOL
+
+    offset, checked, near_ties = 0, 0, 0
+    for r, seq in zip(requests, sequences):
+        first = len(r.prompt_token_ids) - 1
+        rows = ref_logits[offset + first : offset + len(seq)]
+        offset += len(seq)
+        top2 = rows.topk(2, dim=-1)
+        expected = top2.indices[:, 0].tolist()
+        gap = (top2.values[:, 0] - top2.values[:, 1]).tolist()
+        for got, want, g in zip(r.output_token_ids, expected, gap):
+            checked += 1
+            if got != want:
+                near_ties += 1
+                assert g < NEAR_TIE, f"{r.request_id}: token {got} != {want} with a reference logit gap of {g:.4f}"
+    print(f"{checked} positions, {near_ties} near-tie flips")
+    assert checked == 8 * 12
+    assert near_ties <= checked // 10
