@@ -211,7 +211,20 @@ def run_e2e(args, device) -> dict:
     del warm
     torch.cuda.synchronize(device)
 
-    engine = GenerationEngine(model, num_blocks=num_blocks, max_num_batched_tokens=8192, max_num_seqs=256)
+    max_model_len = per_request * block_size
+    engine = GenerationEngine(
+        model,
+        num_blocks=num_blocks,
+        max_num_batched_tokens=8192,
+        max_num_seqs=256,
+        max_model_len=max_model_len,
+        decode_graphs=not args.e2e_eager,
+    )
+    if engine.graphs is not None:
+        # Capture every bucket before timing (the reference captures at start-up, model_runner.py:344-497).
+        for size in engine.graphs.BUCKETS:
+            if size <= 256:
+                engine.graphs.capture(size)
     requests = [Request(f"r{i}", p, max_tokens=args.e2e_max_tokens) for i, p in enumerate(prompts)]
     result = engine.generate(requests)
     return {
@@ -232,12 +245,19 @@ def run_e2e(args, device) -> dict:
                 f"qwen3_e2e: Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads of 128, qk-norm, "
                 f"MLP 3072, vocab 151936, tied embeddings), random init seed 0, bf16; {args.e2e_requests} "
                 f"requests with random prompts U[64,1024], {args.e2e_max_tokens} greedy tokens each, "
-                "max_num_batched_tokens 8192, max_num_seqs 256, block 16, eager"
+                "max_num_batched_tokens 8192, max_num_seqs 256, block 16, "
+                + ("eager" if args.e2e_eager else "decode steps as HIP graphs (buckets 1..256)")
             ),
             "parameters": model.parameter_count(),
             "prompt_tokens": result.prompt_tokens,
             "output_tokens": result.output_tokens,
             "step_seconds": round(result.step_seconds, 4),
+            "decode_steps": result.decode_steps,
+            "decode_step_ms": round(result.decode_seconds / max(result.decode_steps, 1) * 1e3, 3),
+            "other_steps": result.steps - result.decode_steps,
+            "other_step_ms": round(
+                (result.step_seconds - result.decode_seconds) / max(result.steps - result.decode_steps, 1) * 1e3, 3
+            ),
             "preemptions": result.preemptions,
             "parallelism": "single GPU",
         },
@@ -254,6 +274,7 @@ def main() -> int:
     parser.add_argument("--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed", "qwen3_e2e"])
     parser.add_argument("--e2e-requests", type=int, default=256, help="requests of the qwen3_e2e workload")
     parser.add_argument("--e2e-max-tokens", type=int, default=256, help="greedy output tokens per request (qwen3_e2e)")
+    parser.add_argument("--e2e-eager", action="store_true", help="run qwen3_e2e decode steps eagerly (no HIP graphs)")
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")

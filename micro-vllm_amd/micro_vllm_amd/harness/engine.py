@@ -21,6 +21,13 @@ tables (core/block.py:39; model_runner.py:243-245). The step's flattened
 input and attention metadata are built on the GPU
 (`worker.packing.pack_scheduler_output`); sampling runs on the device with
 one device-to-host copy of the sampled token ids per step.
+
+Decode-only steps can run as HIP graphs, one per batch-size bucket, like the
+reference's CUDA-graph execution (model_runner.py:344-497): the packing
+kernels rewrite the bucket's static input buffers (padded the way
+model_runner.py:78-122 pads them: no tokens past the real ones, slot -1,
+null block ids) and the captured forward, greedy argmax included, is
+replayed.
 """
 
 from __future__ import annotations
@@ -33,7 +40,7 @@ import torch
 
 from micro_vllm_amd.attention.spec import FullAttentionSpec
 from micro_vllm_amd.harness.model import DecoderModel
-from micro_vllm_amd.worker.packing import pack_scheduler_output
+from micro_vllm_amd.worker.packing import allocate_packed_batch, pack_scheduler_output
 from micro_vllm_amd.worker.scheduler_output import (
     CacheGroupBlockTable,
     ScheduledRequest,
@@ -71,6 +78,8 @@ class GenerationResult:
     output_tokens: int
     prompt_tokens: int
     preemptions: int
+    decode_steps: int = 0          # steps whose requests all decode one token
+    decode_seconds: float = 0.0
 
     @property
     def output_tokens_per_second(self) -> float:
@@ -88,10 +97,13 @@ class GenerationEngine:
         block_size: int = 16,
         max_num_batched_tokens: int = 8192,
         max_num_seqs: int = 256,
+        max_model_len: int = 8192,
+        decode_graphs: bool = False,
     ) -> None:
         c = model.config
         self.model = model
         self.block_size = block_size
+        self.max_model_len = max_model_len
         self.max_num_batched_tokens = max_num_batched_tokens
         self.max_num_seqs = max_num_seqs
         # Physical pool: ids [0, num_blocks - 1) are allocatable, the last id
@@ -111,6 +123,7 @@ class GenerationEngine:
         self._running: list[Request] = []
         self._requests: dict[str, Request] = {}
         self.preemptions = 0
+        self.graphs = DecodeGraphs(self) if decode_graphs else None
 
     # ------------------------------------------------------------ requests
     def add_request(self, request: Request) -> None:
@@ -118,6 +131,8 @@ class GenerationEngine:
             raise ValueError(f"duplicate request id {request.request_id!r}")
         if not request.prompt_token_ids:
             raise ValueError("a request needs at least one prompt token")
+        if len(request.prompt_token_ids) + request.max_tokens > self.max_model_len:
+            raise ValueError(f"request {request.request_id!r} exceeds max_model_len {self.max_model_len}")
         self._requests[request.request_id] = request
         self._waiting.append(request)
 
@@ -214,6 +229,8 @@ class GenerationEngine:
         """One model step on the GPU; returns the greedy tokens of the
         sampling requests, in plan order."""
 
+        if self.graphs is not None and self.graphs.accepts(plan):
+            return self.graphs.run(plan)
         packed = pack_scheduler_output(
             plan,
             specs=[FullAttentionSpec()],
@@ -235,8 +252,8 @@ class GenerationEngine:
 
         for request in requests:
             self.add_request(request)
-        steps = 0
-        seconds = 0.0
+        steps = decode_steps = 0
+        seconds = decode_seconds = 0.0
         device = self.model.device
         torch.cuda.synchronize(device)
         while self.has_unfinished_requests():
@@ -245,8 +262,12 @@ class GenerationEngine:
             sampled = self.execute(plan)
             torch.cuda.synchronize(device)
             self._update(plan, sampled)
-            seconds += time.perf_counter() - start
+            elapsed = time.perf_counter() - start
+            seconds += elapsed
             steps += 1
+            if all(s.num_scheduled_tokens == 1 for s in plan.scheduled_requests):
+                decode_steps += 1
+                decode_seconds += elapsed
         return GenerationResult(
             outputs={r.request_id: list(r.output_token_ids) for r in requests},
             steps=steps,
@@ -254,4 +275,92 @@ class GenerationEngine:
             output_tokens=sum(len(r.output_token_ids) for r in requests),
             prompt_tokens=sum(len(r.prompt_token_ids) for r in requests),
             preemptions=self.preemptions,
+            decode_steps=decode_steps,
+            decode_seconds=decode_seconds,
         )
+
+
+class DecodeGraphs:
+    """Captured decode steps of one engine, one HIP graph per bucket."""
+
+    BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
+
+    def __init__(self, engine: GenerationEngine) -> None:
+        self.engine = engine
+        self.width = -(-engine.max_model_len // engine.block_size)
+        self.max_batch = self.BUCKETS[-1]
+        self.pool = torch.cuda.graph_pool_handle()
+        self.entries: dict[int, DecodeGraph] = {}
+
+    def accepts(self, plan: SchedulerOutput) -> bool:
+        items = plan.scheduled_requests
+        return (
+            0 < len(items) <= self.max_batch
+            and all(s.num_scheduled_tokens == 1 and s.requires_sampling for s in items)
+        )
+
+    def bucket(self, num_requests: int) -> int:
+        return min(b for b in self.BUCKETS if b >= num_requests)
+
+    def _pack(self, plan: SchedulerOutput, buffers) -> None:
+        e = self.engine
+        pack_scheduler_output(
+            plan,
+            specs=[FullAttentionSpec()],
+            block_size=e.block_size,
+            null_block_id=e.null_block_id,
+            device=e.model.device,
+            into=buffers,
+        )
+
+    def forward(self, buffers) -> tuple[torch.Tensor, torch.Tensor]:
+        """The decode step on a bucket's buffers: logits and greedy token of every row."""
+
+        model = self.engine.model
+        hidden = model.forward(buffers.input_ids, buffers.positions, self.engine.kv_caches, buffers.group_metadata[0])
+        logits = model.logits(hidden)
+        return logits, logits.argmax(dim=-1)
+
+    @torch.inference_mode()
+    def capture(self, size: int) -> "DecodeGraph":
+        e = self.engine
+        buffers = allocate_packed_batch(
+            num_groups=1,
+            block_size=e.block_size,
+            token_capacity=size,
+            request_capacity=size,
+            block_table_widths=[self.width],
+            sampling_capacity=size,
+            device=e.model.device,
+            max_query_len=1,
+        )
+        self._pack(SchedulerOutput(()), buffers)  # an all-padding step: writes nothing
+        side = torch.cuda.Stream(e.model.device)
+        side.wait_stream(torch.cuda.current_stream(e.model.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self.forward(buffers)
+        torch.cuda.current_stream(e.model.device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self.pool):
+            logits, tokens = self.forward(buffers)
+        entry = DecodeGraph(graph, buffers, logits, tokens)
+        self.entries[size] = entry
+        return entry
+
+    @torch.inference_mode()
+    def run(self, plan: SchedulerOutput) -> list[int]:
+        n = len(plan.scheduled_requests)
+        size = self.bucket(n)
+        entry = self.entries.get(size) or self.capture(size)
+        self._pack(plan, entry.buffers)
+        entry.graph.replay()
+        return entry.tokens[:n].tolist()
+
+
+@dataclass
+class DecodeGraph:
+    graph: torch.cuda.CUDAGraph
+    buffers: object   # the bucket's PackedBatch (static inputs)
+    logits: torch.Tensor
+    tokens: torch.Tensor

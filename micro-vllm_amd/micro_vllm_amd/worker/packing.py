@@ -51,12 +51,19 @@ def pack_scheduler_output(
     token_capacity: int | None = None,
     request_capacity: int | None = None,
     block_table_width: int | None = None,
+    into: PackedBatch | None = None,
 ) -> PackedBatch:
     """Pack ``plan`` for every cache group (``specs[g]`` is group g's spec).
 
     Without capacities the outputs have the reference's unpadded shapes
     (block table width = the longest block list of the group). With
     capacities they are padded the way a captured graph expects.
+
+    ``into`` (from ``allocate_packed_batch``) makes the call write into
+    existing tensors, whose shapes set the capacities: a captured graph keeps
+    reading the same buffers while every step re-packs them. The returned
+    batch then shares those tensors (its sampling rows are a prefix view of
+    ``into.sampling_row_indices``).
     """
 
     device = torch.device(device)
@@ -83,6 +90,14 @@ def pack_scheduler_output(
     sampling = np.fromiter((r.requires_sampling for r in requests), dtype=np.int64, count=num_requests)
     num_tokens = int(scheduled.sum())
     num_sampling = int(sampling.sum())
+    if into is not None:
+        if len(into.group_metadata) != num_groups:
+            raise ValueError(f"`into` holds {len(into.group_metadata)} cache groups, the plan needs {num_groups}")
+        token_capacity = into.input_ids.numel()
+        request_capacity = into.group_metadata[0].context_lengths.numel()
+        block_table_width = into.group_metadata[0].block_table.shape[1]
+        if into.sampling_row_indices.numel() < num_sampling:
+            raise ValueError("`into` has too few sampling rows for the plan")
     token_capacity = num_tokens if token_capacity is None else token_capacity
     request_capacity = num_requests if request_capacity is None else request_capacity
     if token_capacity < num_tokens or request_capacity < num_requests:
@@ -124,21 +139,37 @@ def pack_scheduler_output(
         host = torch.zeros(1, dtype=torch.int32)
     payload = host.pin_memory().to(device, non_blocking=True)
 
-    i64 = dict(dtype=torch.int64, device=device)
-    input_ids = torch.empty(token_capacity, **i64)
-    positions = torch.empty(token_capacity, **i64)
-    query_start_locations = torch.empty(request_capacity + 1, **i64)
-    context_lengths = torch.empty(request_capacity, **i64)
-    sampling_rows = torch.empty(num_sampling, **i64)
+    if into is None:
+        into = allocate_packed_batch(
+            num_groups=num_groups,
+            block_size=block_size,
+            token_capacity=token_capacity,
+            request_capacity=request_capacity,
+            block_table_widths=widths,
+            sampling_capacity=num_sampling,
+            device=device,
+            max_query_len=int(scheduled.max()) if num_requests else 0,
+        )
+    else:
+        if any(m.block_table.shape[1] != w for m, w in zip(into.group_metadata, widths)):
+            raise ValueError("`into` block tables do not have the plan's width")
+        hint = into.group_metadata[0].max_query_len
+        if hint is not None and num_requests and int(scheduled.max()) > hint:
+            raise ValueError(f"`into` is for steps of at most {hint} query tokens per request")
+    input_ids = into.input_ids
+    positions = into.positions
+    query_start_locations = into.group_metadata[0].query_start_locations
+    context_lengths = into.group_metadata[0].context_lengths
+    sampling_rows = into.sampling_row_indices
     lib = _native.load()
     stream = _native.stream_handle(device)
     base = payload.data_ptr()
-    metadata = []
     for g, spec in enumerate(specs):
         info_offset, ids_offset, total_blocks = group_layout[g]
-        context_starts = torch.empty(token_capacity, **i64)
-        slot_mapping = torch.empty(token_capacity, **i64)
-        block_table = torch.empty((request_capacity, widths[g]), **i64)
+        group = into.group_metadata[g]
+        context_starts = group.query_context_start_positions
+        slot_mapping = group.slot_mapping
+        block_table = group.block_table
         kind, parameter = spec.kernel_code()
         first = g == 0
         args = _native.PackArgs()
@@ -164,24 +195,51 @@ def pack_scheduler_output(
         args.slot_mapping = slot_mapping.data_ptr() if token_capacity else None
         args.sampling_rows = sampling_rows.data_ptr() if first and num_sampling else None
         _native.check(lib.mvllm_pack_batch(args, stream), "mvllm_pack_batch")
-        metadata.append(
-            AttentionMetadata(
-                query_positions=positions,
-                query_context_start_positions=context_starts,
-                query_start_locations=query_start_locations,
-                context_lengths=context_lengths,
-                block_table=block_table,
-                slot_mapping=slot_mapping,
-                block_size=block_size,
-                max_query_len=int(scheduled.max()) if num_requests else 0,
-            )
-        )
     # `payload` was allocated on the current stream, so the caching allocator
     # reuses its memory only for work ordered after these launches.
     return PackedBatch(
         input_ids=input_ids,
         positions=positions,
-        group_metadata=tuple(metadata),
+        group_metadata=into.group_metadata,
         request_ids=tuple(r.request_id for r in requests),
-        sampling_row_indices=sampling_rows,
+        sampling_row_indices=sampling_rows[:num_sampling],
+    )
+
+
+def allocate_packed_batch(
+    *,
+    num_groups: int,
+    block_size: int,
+    token_capacity: int,
+    request_capacity: int,
+    block_table_widths: Sequence[int],
+    sampling_capacity: int,
+    device: torch.device | str,
+    max_query_len: int | None = None,
+) -> PackedBatch:
+    """Uninitialised device tensors of a packed step at fixed capacities."""
+
+    i64 = dict(dtype=torch.int64, device=torch.device(device))
+    positions = torch.empty(token_capacity, **i64)
+    query_start_locations = torch.empty(request_capacity + 1, **i64)
+    context_lengths = torch.empty(request_capacity, **i64)
+    metadata = tuple(
+        AttentionMetadata(
+            query_positions=positions,
+            query_context_start_positions=torch.empty(token_capacity, **i64),
+            query_start_locations=query_start_locations,
+            context_lengths=context_lengths,
+            block_table=torch.empty((request_capacity, block_table_widths[g]), **i64),
+            slot_mapping=torch.empty(token_capacity, **i64),
+            block_size=block_size,
+            max_query_len=max_query_len,
+        )
+        for g in range(num_groups)
+    )
+    return PackedBatch(
+        input_ids=torch.empty(token_capacity, **i64),
+        positions=positions,
+        group_metadata=metadata,
+        request_ids=(),
+        sampling_row_indices=torch.empty(sampling_capacity, **i64),
     )

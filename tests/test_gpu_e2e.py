@@ -66,15 +66,8 @@ def teacher_forced_logits(model, sequences, device):
     return model.logits(hidden).float()
 
 
-def test_greedy_decoding_matches_reference_attention(device):
-    cfg = DecoderConfig.qwen3_0_6b(num_hidden_layers=2, vocab_size=VOCAB)
-    hip_model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=3)
-    ref_model = DecoderModel(cfg, TorchReferenceAttention(), device=device, seed=3)
-    requests = make_requests(seed=1, count=8, lo=20, hi=200, max_tokens=12)
-    engine = GenerationEngine(hip_model, num_blocks=256, max_num_batched_tokens=160, max_num_seqs=6)
-    result = engine.generate(requests)
-    assert result.output_tokens == 8 * 12
-    assert result.steps > 12  # chunked prefill and mixed steps happened
+def check_against_reference(requests, hip_model, ref_model, device):
+    """Teacher-forced check of every generated position (see module doc)."""
 
     sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in requests]
     ref_logits = teacher_forced_logits(ref_model, sequences, device)
@@ -98,5 +91,65 @@ def test_greedy_decoding_matches_reference_attention(device):
                 near_ties += 1
                 assert g < NEAR_TIE, f"{r.request_id}: token {got} != {want} with a reference logit gap of {g:.4f}"
     print(f"{checked} positions, {near_ties} near-tie flips")
-    assert checked == 8 * 12
     assert near_ties <= checked // 10
+    return checked
+
+
+def models(device, seed=3):
+    cfg = DecoderConfig.qwen3_0_6b(num_hidden_layers=2, vocab_size=VOCAB)
+    hip_model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed)
+    ref_model = DecoderModel(cfg, TorchReferenceAttention(), device=device, seed=seed)
+    return hip_model, ref_model
+
+
+def test_greedy_decoding_matches_reference_attention(device):
+    hip_model, ref_model = models(device)
+    requests = make_requests(seed=1, count=8, lo=20, hi=200, max_tokens=12)
+    engine = GenerationEngine(hip_model, num_blocks=256, max_num_batched_tokens=160, max_num_seqs=6, max_model_len=512)
+    result = engine.generate(requests)
+    assert result.output_tokens == 8 * 12
+    assert result.steps > 12  # chunked prefill and mixed steps happened
+    assert check_against_reference(requests, hip_model, ref_model, device) == 8 * 12
+
+
+def test_greedy_decoding_with_decode_graphs_matches_reference_attention(device):
+    hip_model, ref_model = models(device, seed=5)
+    requests = make_requests(seed=2, count=7, lo=10, hi=150, max_tokens=16)
+    engine = GenerationEngine(
+        hip_model, num_blocks=256, max_num_batched_tokens=512, max_num_seqs=8, max_model_len=512, decode_graphs=True
+    )
+    result = engine.generate(requests)
+    assert result.output_tokens == 7 * 16
+    assert set(engine.graphs.entries) >= {8}  # decode steps ran as graphs
+    check_against_reference(requests, hip_model, ref_model, device)
+
+
+def test_decode_graph_replays_match_eager_on_the_same_buffers(device):
+    """Every replay of a captured decode step equals an eager forward on the
+    same static buffers, bit for bit, with eager work between replays."""
+
+    hip_model, _ = models(device, seed=7)
+    engine = GenerationEngine(
+        hip_model, num_blocks=128, max_num_batched_tokens=1024, max_num_seqs=8, max_model_len=256, decode_graphs=True
+    )
+    for r in make_requests(seed=4, count=5, lo=30, hi=90, max_tokens=8):
+        engine.add_request(r)
+    plan = engine.schedule()  # the prompts, in one step
+    engine._update(plan, engine.execute(plan))
+    plan = engine.schedule()  # a decode step of 5 requests
+    assert engine.graphs.accepts(plan)
+    entry = engine.graphs.capture(engine.graphs.bucket(len(plan.scheduled_requests)))
+    engine.graphs._pack(plan, entry.buffers)
+    torch.cuda.synchronize()
+    with torch.inference_mode():
+        eager_logits, eager_tokens = engine.graphs.forward(entry.buffers)
+    eager_logits, eager_tokens = eager_logits.clone(), eager_tokens.clone()
+    with torch.inference_mode():
+        for _ in range(3):
+            entry.logits.zero_()
+            torch.cuda.synchronize()
+            entry.graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(entry.logits, eager_logits)
+            assert torch.equal(entry.tokens, eager_tokens)
+            _ = (eager_logits.float() * 2).sum().item()  # eager work between replays
