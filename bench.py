@@ -197,7 +197,9 @@ def run_e2e(args, device) -> dict:
     from micro_vllm_amd.harness import DecoderConfig, DecoderModel, GenerationEngine, Request
 
     cfg = DecoderConfig.qwen3_0_6b()
-    model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=0)
+    model = DecoderModel(
+        cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=0, fused_layers=not args.e2e_unfused
+    )
     rng = np.random.default_rng(0)
     lengths = rng.integers(64, 1025, size=args.e2e_requests)
     prompts = [rng.integers(0, cfg.vocab_size, size=int(n)).tolist() for n in lengths]
@@ -247,6 +249,7 @@ def run_e2e(args, device) -> dict:
                 f"requests with random prompts U[64,1024], {args.e2e_max_tokens} greedy tokens each, "
                 "max_num_batched_tokens 8192, max_num_seqs 256, block 16, "
                 + ("eager" if args.e2e_eager else "decode steps as HIP graphs (buckets 1..256)")
+                + ("; torch layers" if args.e2e_unfused else "; fused HIP layer kernels")
             ),
             "parameters": model.parameter_count(),
             "prompt_tokens": result.prompt_tokens,
@@ -275,6 +278,9 @@ def main() -> int:
     parser.add_argument("--e2e-requests", type=int, default=256, help="requests of the qwen3_e2e workload")
     parser.add_argument("--e2e-max-tokens", type=int, default=256, help="greedy output tokens per request (qwen3_e2e)")
     parser.add_argument("--e2e-eager", action="store_true", help="run qwen3_e2e decode steps eagerly (no HIP graphs)")
+    parser.add_argument(
+        "--e2e-unfused", action="store_true", help="qwen3_e2e with the torch layers instead of the fused HIP layer kernels"
+    )
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")

@@ -254,13 +254,56 @@ typedef struct mvllm_pack_args {
 
 int mvllm_pack_batch(const mvllm_pack_args* args, void* stream);
 
+/*
+ * Fused residual add + RMSNorm over `rows` rows of `dim` bf16/fp16 values
+ * (dim <= 8192, strides in elements):
+ *   if residual != NULL: h = round(residual + x), residual <- h; else h = x
+ *   out = round(weight * round(h * rsqrt(mean(h^2) + eps)))
+ * float32 math with the reference's rounding points. Replaces RMSNorm
+ * (layers/normalization.py:7-22) and the decoder layer's residual adds
+ * (models/qwen.py:136-156, models/llama.py:120-140).
+ */
+int mvllm_add_rms_norm(const void* x, int64_t x_stride, void* residual,
+                       int64_t residual_stride, const void* weight, void* out,
+                       int64_t out_stride, int64_t rows, int64_t dim,
+                       float eps, int32_t dtype, void* stream);
+
+/*
+ * Pre-attention step of one layer, head_dim 128: per token, per-head RMSNorm
+ * of query and key (weights may both be NULL: no norm), rotary embedding with
+ * float32 cos/sin tables [num_tokens, 128] (both NULL: none; rotate-half
+ * convention), the rotated query to q_out ([num_tokens, Hq, 128],
+ * contiguous), and the rotated key and the value into their paged-cache slot
+ * (slot < 0 or out of range writes nothing). Replaces Qwen3Attention's q/k
+ * norm + RotaryEmbedding (models/qwen.py:89-91, layers/rotary_embedding.py:
+ * 14-52) followed by write_kv_cache (operators/reference.py:84-98); the
+ * attention that follows is mvllm_paged_attention.
+ */
+int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query,
+                                const mvllm_tensor3* key,
+                                const mvllm_tensor3* value,
+                                const void* q_weight, const void* k_weight,
+                                const float* cos_table, const float* sin_table,
+                                float eps, void* q_out,
+                                const mvllm_kv_cache* cache,
+                                const int64_t* slot_mapping, void* stream);
+
+/*
+ * SwiGLU activation: gate_up rows hold [gate | up] (2 * intermediate values),
+ * out[r, i] = round(round(silu(gate[r, i])) * up[r, i]). Replaces
+ * SwiGLUMLP's silu(gate_proj(x)) * up_proj(x) (layers/mlp.py:10-21).
+ */
+int mvllm_silu_mul(const void* gate_up, int64_t in_stride, void* out,
+                   int64_t out_stride, int64_t rows, int64_t intermediate,
+                   int32_t dtype, void* stream);
+
 /* Text of the last failure on this thread ("" if none). */
 const char* mvllm_last_error(void);
 
 /* ABI version of this header (bumped on incompatible change). */
 int mvllm_abi_version(void);
 
-#define MVLLM_ABI_VERSION 2
+#define MVLLM_ABI_VERSION 3
 
 #ifdef __cplusplus
 }

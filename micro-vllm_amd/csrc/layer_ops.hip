@@ -1,0 +1,310 @@
+// Fused elementwise steps of the decoder layer around the attention call,
+// for bf16 / fp16 activations. Each replaces a chain of framework kernels
+// with one HBM pass and keeps the reference's numerics: float32 math, the
+// same rounding points to the activation type, and the rotary embedding's
+// separately rounded multiplies and add.
+//
+// * add_rms_norm: h = residual + x (rounded), residual <- h,
+//   out = weight * round(h * rsqrt(mean(h^2) + eps))
+//   (layers/normalization.py:7-22; the residual adds of qwen.py:136-156).
+// * qk_norm_rope_kv_write: per token, per-head RMSNorm of q and k (qwen.py:
+//   89-90), rotary embedding with precomputed cos/sin (rotary_embedding.py:
+//   14-52), q to its output, rotated k and v straight into their paged-cache
+//   slot (reference.py:84-98; slot < 0 writes nothing).
+// * silu_mul: out = round(round(silu(gate)) * up) (layers/mlp.py:10-21).
+#include <cmath>
+
+#include "common.h"
+
+namespace mvllm {
+namespace {
+
+template <typename T> struct Act;
+template <> struct Act<bf16_t> {
+  __device__ static float load(uint16_t b) { return bf16_bits_to_float(b); }
+  __device__ static uint16_t store(float v) { return static_cast<uint16_t>(float_to_bf16_bits(v)); }
+  __device__ static float round(float v) { return load(store(v)); }
+};
+template <> struct Act<f16_t> {
+  __device__ static float load(uint16_t b) { return f16_bits_to_float(b); }
+  __device__ static uint16_t store(float v) { return static_cast<uint16_t>(float_to_f16_bits(v)); }
+  __device__ static float round(float v) { return load(store(v)); }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// ------------------------------------------------------------ add_rms_norm
+
+struct NormArgs {
+  const uint16_t* x;
+  uint16_t* residual;  // null: no residual add
+  const uint16_t* weight;
+  uint16_t* out;
+  int64_t x_stride, res_stride, out_stride;
+  int64_t rows;
+  int32_t dim;
+  float eps;
+};
+
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxPerThread = 32;  // dim <= 8192
+
+template <typename T>
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(NormArgs a) {
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint16_t* x = a.x + row * a.x_stride;
+  uint16_t* res = a.residual ? a.residual + row * a.res_stride : nullptr;
+  float h[kNormMaxPerThread];
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxPerThread; ++i) {
+    const int d = tid + i * kNormThreads;
+    h[i] = 0.f;
+    if (d < a.dim) {
+      float v = Act<T>::load(x[d]);
+      if (res) {
+        v = Act<T>::round(Act<T>::load(res[d]) + v);
+        res[d] = Act<T>::store(v);
+      }
+      h[i] = v;
+      sq = __builtin_fmaf(v, v, sq);
+    }
+  }
+  __shared__ float partial[kNormThreads / 64];
+  sq = wave_sum(sq);
+  if ((tid & 63) == 0) partial[tid >> 6] = sq;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / 64; ++w) total += partial[w];
+  const float inv = 1.f / sqrtf(total / static_cast<float>(a.dim) + a.eps);
+  uint16_t* out = a.out + row * a.out_stride;
+#pragma unroll
+  for (int i = 0; i < kNormMaxPerThread; ++i) {
+    const int d = tid + i * kNormThreads;
+    if (d < a.dim) {
+      const float normed = Act<T>::round(h[i] * inv);
+      out[d] = Act<T>::store(Act<T>::load(a.weight[d]) * normed);
+    }
+  }
+}
+
+// --------------------------------------------------- qk_norm_rope_kv_write
+
+struct QkArgs {
+  const uint16_t* q;  // [N, Hq, D] strided
+  const uint16_t* k;  // [N, Hkv, D] strided
+  const uint16_t* v;  // [N, Hkv, D] strided
+  int64_t q_s0, q_s1, k_s0, k_s1, v_s0, v_s1;
+  const uint16_t* q_weight;  // [D] or null (no q/k norm)
+  const uint16_t* k_weight;
+  const float* cos;  // [N, D] or null (no rotary embedding)
+  const float* sin;
+  uint16_t* q_out;  // [N, Hq, D] contiguous
+  uint16_t* cache;
+  int64_t c_s[5];
+  const int64_t* slots;
+  int64_t num_tokens, num_slots, block_size;
+  int32_t num_q_heads, num_kv_heads;
+  float eps;
+};
+
+// One wave per (token, row); rows 0..Hq-1 are query heads, then Hkv key
+// heads, then Hkv value heads. head_dim 128: lane l holds dims 2l, 2l+1, so
+// the rotate-half partner of lane l's pair sits in lane l ^ 32.
+template <typename T>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int rows = a.num_q_heads + 2 * a.num_kv_heads;
+  const int64_t t = item / rows;
+  const int row = static_cast<int>(item % rows);
+  if (t >= a.num_tokens) return;
+  const bool is_q = row < a.num_q_heads;
+  const bool is_v = row >= a.num_q_heads + a.num_kv_heads;
+  const int head = is_q ? row : is_v ? row - a.num_q_heads - a.num_kv_heads : row - a.num_q_heads;
+  const uint16_t* src = is_q ? a.q + t * a.q_s0 + head * a.q_s1
+                      : is_v ? a.v + t * a.v_s0 + head * a.v_s1
+                             : a.k + t * a.k_s0 + head * a.k_s1;
+  const uint32_t pair = *reinterpret_cast<const uint32_t*>(src + 2 * lane);
+  uint32_t result = pair;
+  if (!is_v) {
+    float x0 = Act<T>::load(pair & 0xFFFFu), x1 = Act<T>::load(pair >> 16);
+    const uint16_t* w = is_q ? a.q_weight : a.k_weight;
+    if (w) {
+      const float sq = wave_sum(__builtin_fmaf(x0, x0, x1 * x1));
+      const float inv = 1.f / sqrtf(sq / 128.f + a.eps);
+      const uint32_t wp = *reinterpret_cast<const uint32_t*>(w + 2 * lane);
+      x0 = Act<T>::round(Act<T>::load(wp & 0xFFFFu) * Act<T>::round(x0 * inv));
+      x1 = Act<T>::round(Act<T>::load(wp >> 16) * Act<T>::round(x1 * inv));
+    }
+    if (a.cos) {
+      const float p0 = __shfl_xor(x0, 32, 64), p1 = __shfl_xor(x1, 32, 64);
+      // rotate_half: dims < 64 take -x[d + 64], dims >= 64 take x[d - 64].
+      const float r0 = lane < 32 ? -p0 : p0, r1 = lane < 32 ? -p1 : p1;
+      const float2 c = *reinterpret_cast<const float2*>(a.cos + t * 128 + 2 * lane);
+      const float2 s = *reinterpret_cast<const float2*>(a.sin + t * 128 + 2 * lane);
+      x0 = __fadd_rn(__fmul_rn(x0, c.x), __fmul_rn(r0, s.x));
+      x1 = __fadd_rn(__fmul_rn(x1, c.y), __fmul_rn(r1, s.y));
+    }
+    result = static_cast<uint32_t>(Act<T>::store(x0)) | (static_cast<uint32_t>(Act<T>::store(x1)) << 16);
+  }
+  if (is_q) {
+    *reinterpret_cast<uint32_t*>(a.q_out + (t * a.num_q_heads + head) * 128 + 2 * lane) = result;
+    return;
+  }
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.num_slots) return;
+  const int64_t block = slot / a.block_size;
+  const int64_t off = slot - block * a.block_size;
+  uint16_t* dst = a.cache + (is_v ? a.c_s[0] : 0) + block * a.c_s[1] + off * a.c_s[2] + head * a.c_s[3];
+  *reinterpret_cast<uint32_t*>(dst + 2 * lane) = result;
+}
+
+// --------------------------------------------------------------- silu_mul
+
+struct SiluArgs {
+  const uint16_t* gate_up;  // [N, 2I]: gate then up
+  uint16_t* out;            // [N, I]
+  int64_t in_stride, out_stride;
+  int64_t rows;
+  int32_t inter;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(SiluArgs a) {
+  const int64_t row = blockIdx.y;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 2;
+  if (i >= a.inter) return;
+  const uint16_t* g = a.gate_up + row * a.in_stride;
+  const uint32_t gp = *reinterpret_cast<const uint32_t*>(g + i);
+  const uint32_t up = *reinterpret_cast<const uint32_t*>(g + a.inter + i);
+  float r[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float x = Act<T>::load(e ? gp >> 16 : gp & 0xFFFFu);
+    const float s = Act<T>::round(x / (1.f + expf(-x)));
+    r[e] = s * Act<T>::load(e ? up >> 16 : up & 0xFFFFu);
+  }
+  *reinterpret_cast<uint32_t*>(a.out + row * a.out_stride + i) =
+      static_cast<uint32_t>(Act<T>::store(r[0])) | (static_cast<uint32_t>(Act<T>::store(r[1])) << 16);
+}
+
+bool half_dtype(int32_t d) { return d == MVLLM_DTYPE_BF16 || d == MVLLM_DTYPE_F16; }
+
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+}  // namespace
+}  // namespace mvllm
+
+using namespace mvllm;
+
+extern "C" int mvllm_add_rms_norm(const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+                                  const void* weight, void* out, int64_t out_stride, int64_t rows,
+                                  int64_t dim, float eps, int32_t dtype, void* stream) {
+  clear_error();
+  if (!half_dtype(dtype)) return fail(MVLLM_ERR_UNSUPPORTED, "add_rms_norm needs bf16 or fp16");
+  if (rows < 0 || dim <= 0 || dim > kNormThreads * kNormMaxPerThread)
+    return fail(MVLLM_ERR_INVALID, "add_rms_norm: rows %lld / dim %lld out of range", (long long)rows,
+                (long long)dim);
+  if (rows == 0) return MVLLM_OK;
+  if (!x || !weight || !out) return fail(MVLLM_ERR_INVALID, "add_rms_norm: null pointer");
+  if (rows > INT32_MAX) return fail(MVLLM_ERR_INVALID, "add_rms_norm: too many rows");
+  NormArgs a{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(residual),
+             static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), x_stride, residual_stride,
+             out_stride, rows, static_cast<int32_t>(dim), eps};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MVLLM_DTYPE_BF16)
+    hipLaunchKernelGGL(add_rms_norm_kernel<bf16_t>, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(add_rms_norm_kernel<f16_t>, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, s, a);
+  MVLLM_LAUNCH_CHECK("add_rms_norm_kernel");
+  return MVLLM_OK;
+}
+
+extern "C" int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query, const mvllm_tensor3* key,
+                                           const mvllm_tensor3* value, const void* q_weight,
+                                           const void* k_weight, const float* cos_table,
+                                           const float* sin_table, float eps, void* q_out,
+                                           const mvllm_kv_cache* cache, const int64_t* slot_mapping,
+                                           void* stream) {
+  clear_error();
+  if (!query || !key || !value || !cache) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: null descriptor");
+  const int32_t dtype = query->dtype;
+  if (!half_dtype(dtype) || key->dtype != dtype || value->dtype != dtype || cache->dtype != dtype)
+    return fail(MVLLM_ERR_UNSUPPORTED, "qk_norm_rope needs bf16 or fp16 throughout");
+  const int64_t N = query->size[0];
+  if (query->size[2] != 128 || key->size[2] != 128 || value->size[2] != 128 || cache->head_dim != 128)
+    return fail(MVLLM_ERR_UNSUPPORTED, "qk_norm_rope needs head_dim 128");
+  if (key->size[0] != N || value->size[0] != N || key->size[1] != value->size[1] ||
+      key->size[1] != cache->num_kv_heads)
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: query/key/value/cache shapes disagree");
+  if (query->stride[2] != 1 || key->stride[2] != 1 || value->stride[2] != 1 || cache->stride[4] != 1 ||
+      (query->stride[0] | query->stride[1] | key->stride[0] | key->stride[1] | value->stride[0] |
+       value->stride[1] | cache->stride[0] | cache->stride[1] | cache->stride[2] | cache->stride[3]) & 1)
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: rows must be contiguous with even strides");
+  if ((cos_table == nullptr) != (sin_table == nullptr) || (q_weight == nullptr) != (k_weight == nullptr))
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: cos/sin and q/k weights come in pairs");
+  if (N == 0) return MVLLM_OK;
+  if (!slot_mapping || !q_out || !cache->data || !aligned4(query->data) || !aligned4(key->data) ||
+      !aligned4(value->data) || !aligned4(q_out) || !aligned4(cache->data))
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: null or misaligned pointer");
+  QkArgs a = {};
+  a.q = static_cast<const uint16_t*>(query->data);
+  a.k = static_cast<const uint16_t*>(key->data);
+  a.v = static_cast<const uint16_t*>(value->data);
+  a.q_s0 = query->stride[0]; a.q_s1 = query->stride[1];
+  a.k_s0 = key->stride[0]; a.k_s1 = key->stride[1];
+  a.v_s0 = value->stride[0]; a.v_s1 = value->stride[1];
+  a.q_weight = static_cast<const uint16_t*>(q_weight);
+  a.k_weight = static_cast<const uint16_t*>(k_weight);
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.cache = static_cast<uint16_t*>(cache->data);
+  for (int i = 0; i < 5; ++i) a.c_s[i] = cache->stride[i];
+  a.slots = slot_mapping;
+  a.num_tokens = N;
+  a.num_slots = cache->num_blocks * cache->block_size;
+  a.block_size = cache->block_size;
+  a.num_q_heads = static_cast<int32_t>(query->size[1]);
+  a.num_kv_heads = static_cast<int32_t>(key->size[1]);
+  a.eps = eps;
+  const int64_t items = N * (query->size[1] + 2 * key->size[1]);
+  const int64_t blocks = (items + 3) / 4;
+  if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: grid too large");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MVLLM_DTYPE_BF16)
+    hipLaunchKernelGGL(qk_norm_rope_kernel<bf16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_kernel<f16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+  MVLLM_LAUNCH_CHECK("qk_norm_rope_kernel");
+  return MVLLM_OK;
+}
+
+extern "C" int mvllm_silu_mul(const void* gate_up, int64_t in_stride, void* out, int64_t out_stride,
+                              int64_t rows, int64_t intermediate, int32_t dtype, void* stream) {
+  clear_error();
+  if (!half_dtype(dtype)) return fail(MVLLM_ERR_UNSUPPORTED, "silu_mul needs bf16 or fp16");
+  if (rows < 0 || intermediate <= 0 || (intermediate & 1) || (in_stride & 1) || (out_stride & 1))
+    return fail(MVLLM_ERR_INVALID, "silu_mul: sizes and strides must be even");
+  if (rows == 0) return MVLLM_OK;
+  if (!gate_up || !out || !aligned4(gate_up) || !aligned4(out))
+    return fail(MVLLM_ERR_INVALID, "silu_mul: null or misaligned pointer");
+  if (rows > 65535) return fail(MVLLM_ERR_INVALID, "silu_mul: more than 65535 rows");
+  SiluArgs a{static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), in_stride, out_stride, rows,
+             static_cast<int32_t>(intermediate)};
+  const dim3 grid(static_cast<unsigned>((intermediate / 2 + 255) / 256), static_cast<unsigned>(rows));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MVLLM_DTYPE_BF16)
+    hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<f16_t>, grid, dim3(256), 0, s, a);
+  MVLLM_LAUNCH_CHECK("silu_mul_kernel");
+  return MVLLM_OK;
+}

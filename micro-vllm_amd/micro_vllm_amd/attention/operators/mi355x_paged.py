@@ -174,6 +174,42 @@ def hip_paged_attention(
     return output
 
 
+def hip_attention_over_cache(
+    query: torch.Tensor,
+    layer_kv_cache: torch.Tensor,
+    metadata: AttentionMetadata,
+) -> torch.Tensor:
+    """Ragged causal attention over a cache that already holds the step's
+    K/V (written by ``layers.qk_norm_rope_kv_write``): the attention part of
+    ``hip_paged_attention``, without the cache write."""
+
+    if query.device.type != "cuda" or layer_kv_cache.device != query.device:
+        raise RuntimeError("mi355x_paged attention requires GPU tensors on one device")
+    if query.dtype not in SUPPORTED_DTYPES or layer_kv_cache.dtype != query.dtype:
+        raise ValueError(f"unsupported or mismatched dtypes {query.dtype} / {layer_kv_cache.dtype}")
+    device = query.device
+    batch, keep = batch_descriptor(metadata, device)
+    output = torch.empty_like(query)
+    lib = _native.load()
+    workspace_bytes = lib.mvllm_attention_workspace_bytes(batch, query.shape[1], query.shape[2])
+    workspace = torch.empty(max(workspace_bytes, 1), dtype=torch.uint8, device=device)
+    _native.check(
+        lib.mvllm_paged_attention(
+            _native.tensor3(query),
+            _native.kv_cache(layer_kv_cache),
+            batch,
+            _native.tensor3(output),
+            1.0 / math.sqrt(query.shape[-1]),
+            workspace.data_ptr(),
+            workspace.numel(),
+            _native.stream_handle(device),
+        ),
+        "mvllm_paged_attention",
+    )
+    del keep
+    return output
+
+
 def hip_gather_kv_cache(
     layer_kv_cache: torch.Tensor,
     metadata: AttentionMetadata,

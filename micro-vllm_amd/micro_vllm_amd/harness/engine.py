@@ -57,13 +57,23 @@ class Request:
     num_computed_tokens: int = 0
     block_ids: list[int] = field(default_factory=list)
 
-    @property
-    def all_token_ids(self) -> list[int]:
-        return self.prompt_token_ids + self.output_token_ids
+    def __post_init__(self) -> None:
+        # Prompt followed by the outputs, grown in place (no per-step copies).
+        self.token_ids: list[int] = list(self.prompt_token_ids) + list(self.output_token_ids)
+        self._block_tuple: tuple[int, ...] | None = None
+
+    def append_output(self, token: int) -> None:
+        self.output_token_ids.append(token)
+        self.token_ids.append(token)
+
+    def block_tuple(self) -> tuple[int, ...]:
+        if self._block_tuple is None or len(self._block_tuple) != len(self.block_ids):
+            self._block_tuple = tuple(self.block_ids)
+        return self._block_tuple
 
     @property
     def num_known_tokens(self) -> int:
-        return len(self.prompt_token_ids) + len(self.output_token_ids)
+        return len(self.token_ids)
 
     @property
     def finished(self) -> bool:
@@ -152,18 +162,18 @@ class GenerationEngine:
     def _free(self, request: Request) -> None:
         self._free_blocks.extend(request.block_ids)
         request.block_ids = []
+        request._block_tuple = None
 
     # ----------------------------------------------------------- schedule
     def _scheduled(self, request: Request, num_tokens: int) -> ScheduledRequest:
         start = request.num_computed_tokens
-        tokens = request.all_token_ids[start : start + num_tokens]
         return ScheduledRequest(
             request_id=request.request_id,
-            input_token_ids=tuple(tokens),
+            input_token_ids=tuple(request.token_ids[start : start + num_tokens]),
             num_computed_tokens=start,
             num_scheduled_tokens=num_tokens,
             requires_sampling=start + num_tokens == request.num_known_tokens,
-            block_tables=(CacheGroupBlockTable(tuple(request.block_ids)),),
+            block_tables=(CacheGroupBlockTable(request.block_tuple()),),
         )
 
     def schedule(self) -> SchedulerOutput:
@@ -171,9 +181,12 @@ class GenerationEngine:
         scheduled: list[ScheduledRequest] = []
         preempted: list[str] = []
         exhausted = False
-        for request in list(self._running):
-            if request not in self._running:
-                continue  # preempted as a victim earlier in this loop
+        index = 0
+        # Victims are popped from the end, so every request before `index`
+        # stays in place.
+        while index < len(self._running):
+            request = self._running[index]
+            index += 1
             if budget == 0 or len(scheduled) == self.max_num_seqs:
                 break
             n = min(request.num_known_tokens - request.num_computed_tokens, budget)
@@ -218,7 +231,7 @@ class GenerationEngine:
             request = self._requests[item.request_id]
             request.num_computed_tokens += item.num_scheduled_tokens
             if item.requires_sampling:
-                request.output_token_ids.append(next(samples))
+                request.append_output(next(samples))
                 if request.finished:
                     self._running.remove(request)
                     self._free(request)

@@ -17,6 +17,12 @@ The q/k/v and gate/up projections are stored as single fused weights so that
 each is one GEMM; every output column is the same dot product as in the
 unfused layers. Weights are drawn from a seeded normal distribution (there is
 no checkpoint to load).
+
+With ``fused_layers=True`` the elementwise steps run as the HIP library's
+fused kernels (`micro_vllm_amd.layers`): residual add + RMSNorm, q/k norm +
+rotary embedding + paged-cache write, SwiGLU, followed by attention over the
+cache (`hip_attention_over_cache`). The torch path stays the restatement the
+fused kernels are checked against.
 """
 
 from __future__ import annotations
@@ -113,9 +119,11 @@ class DecoderModel:
         seed: int = 0,
         init_std: float = 0.02,
         lm_head_std: float | None = None,
+        fused_layers: bool = False,
     ) -> None:
         self.config = config
         self.operator = operator
+        self.fused_layers = fused_layers
         self.device = torch.device(device)
         self.dtype = dtype
         c = config
@@ -175,6 +183,8 @@ class DecoderModel:
     ) -> torch.Tensor:
         """Final hidden states [tokens, hidden] of the flattened batch."""
 
+        if self.fused_layers:
+            return self._forward_fused(input_ids, positions, kv_caches, metadata)
         c = self.config
         eps = c.rms_norm_eps
         n = input_ids.shape[0]
@@ -200,6 +210,50 @@ class DecoderModel:
             gate, up = F.linear(x, layer["gate_up"]).chunk(2, dim=-1)
             hidden = hidden + F.linear(F.silu(gate) * up, layer["down"])
         return rms_norm(hidden, self.final_norm, eps)
+
+    def _forward_fused(
+        self,
+        input_ids: torch.Tensor,
+        positions: torch.Tensor,
+        kv_caches: list[torch.Tensor],
+        metadata: AttentionMetadata,
+    ) -> torch.Tensor:
+        from micro_vllm_amd import layers
+        from micro_vllm_amd.attention.operators.mi355x_paged import hip_attention_over_cache
+
+        c = self.config
+        eps = c.rms_norm_eps
+        n = input_ids.shape[0]
+        q_size = c.num_attention_heads * c.head_dim
+        kv_size = c.num_key_value_heads * c.head_dim
+        cosine, sine = self.rotary_tables(positions)
+        cosine = cosine.reshape(n, c.head_dim).contiguous()
+        sine = sine.reshape(n, c.head_dim).contiguous()
+        residual = F.embedding(input_ids, self.embed)
+        x = layers.add_rms_norm(residual, self.layers[0]["input_norm"], eps)
+        for i, (layer, cache) in enumerate(zip(self.layers, kv_caches)):
+            qkv = F.linear(x, layer["qkv"])
+            q = qkv[:, :q_size].view(n, c.num_attention_heads, c.head_dim)
+            k = qkv[:, q_size : q_size + kv_size].view(n, c.num_key_value_heads, c.head_dim)
+            v = qkv[:, q_size + kv_size :].view(n, c.num_key_value_heads, c.head_dim)
+            q = layers.qk_norm_rope_kv_write(
+                q,
+                k,
+                v,
+                layer["q_norm"] if c.qk_norm else None,
+                layer["k_norm"] if c.qk_norm else None,
+                cosine,
+                sine,
+                eps,
+                cache,
+                metadata.slot_mapping,
+            )
+            attention = hip_attention_over_cache(q, cache, metadata)
+            x = layers.add_rms_norm(F.linear(attention.flatten(1), layer["o"]), layer["post_norm"], eps, residual)
+            mlp = F.linear(layers.silu_mul(F.linear(x, layer["gate_up"])), layer["down"])
+            next_norm = self.layers[i + 1]["input_norm"] if i + 1 < len(self.layers) else self.final_norm
+            x = layers.add_rms_norm(mlp, next_norm, eps, residual)
+        return x
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return F.linear(hidden, self.lm_head)

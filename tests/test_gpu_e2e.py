@@ -95,9 +95,11 @@ def check_against_reference(requests, hip_model, ref_model, device):
     return checked
 
 
-def models(device, seed=3):
-    cfg = DecoderConfig.qwen3_0_6b(num_hidden_layers=2, vocab_size=VOCAB)
-    hip_model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed)
+def models(device, seed=3, fused_layers=False, **overrides):
+    cfg = DecoderConfig.qwen3_0_6b(num_hidden_layers=2, vocab_size=VOCAB, **overrides)
+    hip_model = DecoderModel(
+        cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed, fused_layers=fused_layers
+    )
     ref_model = DecoderModel(cfg, TorchReferenceAttention(), device=device, seed=seed)
     return hip_model, ref_model
 
@@ -121,6 +123,22 @@ def test_greedy_decoding_with_decode_graphs_matches_reference_attention(device):
     result = engine.generate(requests)
     assert result.output_tokens == 7 * 16
     assert set(engine.graphs.entries) >= {8}  # decode steps ran as graphs
+    check_against_reference(requests, hip_model, ref_model, device)
+
+
+@pytest.mark.parametrize("qk_norm", [True, False], ids=["qwen3", "llama3-style"])
+def test_fused_layer_kernels_match_reference_decoding(device, qk_norm):
+    """The fused residual/RMSNorm, q/k-norm + rotary + cache-write and SwiGLU
+    kernels, with decode steps as graphs, against the torch layers and the
+    reference-semantics operator."""
+
+    hip_model, ref_model = models(device, seed=9, fused_layers=True, qk_norm=qk_norm)
+    requests = make_requests(seed=6, count=7, lo=10, hi=160, max_tokens=12)
+    engine = GenerationEngine(
+        hip_model, num_blocks=256, max_num_batched_tokens=200, max_num_seqs=8, max_model_len=512, decode_graphs=True
+    )
+    result = engine.generate(requests)
+    assert result.output_tokens == 7 * 12
     check_against_reference(requests, hip_model, ref_model, device)
 
 

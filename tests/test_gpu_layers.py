@@ -1,0 +1,131 @@
+"""Fused decoder-layer kernels against the torch restatement of the
+reference layers (RMSNorm, residual add, q/k norm + rotary embedding + cache
+write, SwiGLU).
+
+The bar: residual updates, value copies and cache placement are bit-exact.
+Normalised and activated values are within one rounding step of the
+activation type (the kernels accumulate the RMSNorm sum of squares in a
+different order than torch's reduction, and call the device's own
+transcendental functions) and at least 99% are bit-identical; rotated values
+are within one step of the rotation inputs' magnitude plus one of the output,
+and at least 98% are bit-identical.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from micro_vllm_amd import layers
+from micro_vllm_amd.harness.model import _rotate_half, rms_norm
+
+pytestmark = pytest.mark.gpu
+
+ULP = {torch.bfloat16: 2.0**-7, torch.float16: 2.0**-10}
+
+
+def assert_within_one_step(got, want, dtype, min_exact=0.99):
+    got32, want32 = got.float(), want.float()
+    bound = ULP[dtype] * want32.abs().clamp_min(2.0**-6) * 1.01
+    assert torch.all((got32 - want32).abs() <= bound), (got32 - want32).abs().max().item()
+    exact = (got == want).float().mean().item()
+    assert exact >= min_exact, exact
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("rows", "dim"), [(37, 1024), (5, 4096), (1, 128)])
+def test_add_rms_norm_matches_torch(device, dtype, rows, dim):
+    gen = torch.Generator(device=device).manual_seed(rows + dim)
+    x = torch.randn((rows, dim), generator=gen, device=device).to(dtype)
+    res = torch.randn((rows, dim), generator=gen, device=device).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim, generator=gen, device=device)).to(dtype)
+    out = layers.add_rms_norm(x, w, 1e-6)
+    assert_within_one_step(out, rms_norm(x, w, 1e-6), dtype)
+
+    res_before = res.clone()
+    out = layers.add_rms_norm(x, w, 1e-6, residual=res)
+    summed = res_before + x
+    assert torch.equal(res, summed)  # the residual add rounds exactly as torch's
+    assert_within_one_step(out, rms_norm(summed, w, 1e-6), dtype)
+
+
+def test_add_rms_norm_on_a_strided_view(device):
+    gen = torch.Generator(device=device).manual_seed(3)
+    base = torch.randn((9, 3000), generator=gen, device=device).to(torch.bfloat16)
+    x = base[:, 100:2148]
+    w = torch.ones(2048, device=device, dtype=torch.bfloat16)
+    assert_within_one_step(layers.add_rms_norm(x, w, 1e-6), rms_norm(x, w, 1e-6), torch.bfloat16)
+
+
+def torch_qk_rope(x, w, cos, sin, eps):
+    """Reference q/k path; also the magnitude |x.cos| + |rot(x).sin| of the
+    rotation's inputs: a one-step difference in the normalised input (the
+    RMSNorm sum is accumulated in another order) moves the rotated value by
+    up to one step of that magnitude, which exceeds a step of the output
+    when the two terms cancel."""
+
+    if w is not None:
+        x = rms_norm(x, w, eps)
+    x32 = x.float()
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    rotated = (x32 * c + _rotate_half(x32) * s).to(x.dtype)
+    magnitude = (x32 * c).abs() + (_rotate_half(x32) * s).abs()
+    return rotated, magnitude
+
+
+def assert_rotation_close(got, want, magnitude, dtype, min_exact=0.98):
+    got32, want32 = got.float(), want.float()
+    bound = ULP[dtype] * (magnitude + want32.abs()) * 1.01 + ULP[dtype] * 2.0**-14
+    assert torch.all((got32 - want32).abs() <= bound), ((got32 - want32).abs() - bound).max().item()
+    exact = (got == want).float().mean().item()
+    assert exact >= min_exact, exact
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("qk_norm", [True, False], ids=["qwen3", "llama3"])
+def test_qk_norm_rope_kv_write_matches_torch(device, dtype, qk_norm):
+    n, hq, hkv, d, bs, nb = 23, 16, 8, 128, 16, 7
+    gen = torch.Generator(device=device).manual_seed(11)
+    qkv = torch.randn((n, (hq + 2 * hkv) * d), generator=gen, device=device).to(dtype)
+    q = qkv[:, : hq * d].view(n, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].view(n, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].view(n, hkv, d)
+    qw = (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(dtype) if qk_norm else None
+    kw = (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(dtype) if qk_norm else None
+    positions = torch.randint(0, 5000, (n,), generator=gen, device=device)
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32, device=device) / d))
+    freqs = torch.outer(positions.float(), inv)
+    angles = torch.cat((freqs, freqs), dim=-1)
+    cos, sin = angles.cos().contiguous(), angles.sin().contiguous()
+    cache = torch.full((2, nb, bs, hkv, d), float("nan"), dtype=dtype, device=device)
+    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(2))[:n].to(device)
+    slots[[3, 17]] = -1  # padding: writes nothing
+    q_out = layers.qk_norm_rope_kv_write(q, k, v, qw, kw, cos, sin, 1e-6, cache, slots)
+
+    want_q, q_mag = torch_qk_rope(q, qw, cos, sin, 1e-6)
+    want_k, k_mag = torch_qk_rope(k, kw, cos, sin, 1e-6)
+    assert_rotation_close(q_out, want_q, q_mag, dtype)
+    flat = cache.view(2, -1, hkv, d)
+    keep = slots >= 0
+    assert_rotation_close(flat[0, slots[keep]], want_k[keep], k_mag[keep], dtype)
+    assert torch.equal(flat[1, slots[keep]], v[keep])
+    untouched = torch.ones(nb * bs, dtype=torch.bool, device=device)
+    untouched[slots[keep]] = False
+    assert torch.isnan(flat[:, untouched]).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_silu_mul_matches_torch(device, dtype):
+    gen = torch.Generator(device=device).manual_seed(5)
+    gate_up = (3 * torch.randn((19, 2 * 3072), generator=gen, device=device)).to(dtype)
+    gate, up = gate_up.chunk(2, dim=-1)
+    assert_within_one_step(layers.silu_mul(gate_up), F.silu(gate) * up, dtype)
+
+
+def test_fused_ops_reject_unsupported_inputs(device):
+    x = torch.randn((4, 64), device=device)
+    with pytest.raises(ValueError):
+        layers.add_rms_norm(x, torch.ones(64, device=device), 1e-6)  # float32
+    with pytest.raises(ValueError):
+        layers.silu_mul(torch.randn((4, 6), device=device, dtype=torch.bfloat16))
