@@ -27,6 +27,10 @@ struct AttnArgs {
   float2* ws_ml;
   int32_t split_tokens, max_splits;
   int32_t mode;  // generic kernel: 0 = every token; 1 = only requests with > 1 query
+  // Prefill work list: (request, query block) per slot, heaviest first;
+  // request -1 marks an empty slot. Written by the item kernel before the
+  // prefill kernel reads it.
+  int2* items;
 };
 
 // Visible key positions [lo, hi] of query `t` in request `r` whose first

@@ -49,6 +49,8 @@ struct DecodeLayout {
   int32_t max_splits;
   int64_t acc_bytes;
   int64_t ml_bytes;
+  int64_t items_bytes;  // prefill work list: one int2 per slot, N / 8 + R slots at most
+  int64_t total() const { return acc_bytes + ml_bytes + items_bytes; }
 };
 
 DecodeLayout decode_layout(const mvllm_batch* b, int64_t num_q_heads, int64_t head_dim) {
@@ -61,6 +63,8 @@ DecodeLayout decode_layout(const mvllm_batch* b, int64_t num_q_heads, int64_t he
   const int64_t items = b->num_requests * d.max_splits * num_q_heads;
   d.acc_bytes = (items * head_dim * 4 + 255) / 256 * 256;
   d.ml_bytes = (items * 8 + 255) / 256 * 256;
+  // Prefill query blocks hold T = 128 / G >= 8 tokens.
+  d.items_bytes = ((b->num_tokens / 8 + b->num_requests) * 8 + 255) / 256 * 256;
   return d;
 }
 
@@ -102,8 +106,7 @@ extern "C" int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch, int
   if (!batch || num_q_heads <= 0 || head_dim <= 0 || batch->num_requests <= 0 ||
       batch->block_size <= 0)
     return 0;
-  const DecodeLayout d = decode_layout(batch, num_q_heads, head_dim);
-  return d.acc_bytes + d.ml_bytes;
+  return decode_layout(batch, num_q_heads, head_dim).total();
 }
 
 namespace mvllm {
@@ -173,14 +176,15 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
     return launch_generic(a, dtype, s);
   }
   const DecodeLayout d = decode_layout(batch, Hq, D);
-  if (workspace_bytes < d.acc_bytes + d.ml_bytes || (!workspace && d.acc_bytes + d.ml_bytes > 0))
+  if (workspace_bytes < d.total() || (!workspace && d.total() > 0))
     return fail(MVLLM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld required",
-                (long long)workspace_bytes, (long long)(d.acc_bytes + d.ml_bytes));
+                (long long)workspace_bytes, (long long)d.total());
   if (!aligned16(workspace)) return fail(MVLLM_ERR_INVALID, "workspace must be 16-byte aligned");
   a.split_tokens = d.split_tokens;
   a.max_splits = d.max_splits;
   a.ws_acc = static_cast<float*>(workspace);
   a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + d.acc_bytes);
+  a.items = reinterpret_cast<int2*>(static_cast<char*>(workspace) + d.acc_bytes + d.ml_bytes);
   hipEvent_t ds = timing ? static_cast<hipEvent_t>(timing->decode_start) : nullptr;
   hipEvent_t de = timing ? static_cast<hipEvent_t>(timing->decode_stop) : nullptr;
   hipEvent_t ps = timing ? static_cast<hipEvent_t>(timing->prefill_start) : nullptr;

@@ -5,17 +5,18 @@
 // four waves. The workgroup's 128 rows are (query head of the KV head's
 // group, token) pairs: row f -> head f / T, token f % T with T = 128 / G, so
 // all G query heads that share a KV head (GQA) read each K/V tile once.
-// Each wave owns 32 rows.
+// Each wave owns 32 rows. A small kernel lists the items on the GPU, sorted
+// by their number of key tiles, heaviest first (prefill_items_kernel).
 //
 // Keys are processed in tiles of 64 (four 16-token pages). Each wave moves
 // one page of K and of V per tile straight from HBM into LDS
 // (global_load_lds_dwordx4) into double-buffered K and V tiles: the loads of
-// tile k+1 are in flight while tile k is computed, with one barrier per tile.
-// The block ids of a tile's four pages are read from an LDS copy of the
-// block-table row one iteration ahead, so no table lookup sits on the
-// critical path. The K fragments of a tile are read in batches ahead of their
-// MFMAs, and the V operands of the first two 16-key steps are in flight
-// during the softmax.
+// tile k+1 are issued between the MFMAs of tile k (a burst of loads would
+// stall the issuing wave) and land before the tile's one barrier. The block
+// ids of a tile's four pages are read from an LDS copy of the block-table row
+// one iteration ahead, so no table lookup sits on the critical path. Each
+// tile is computed as two halves of 32 keys, each a full online-softmax
+// update; that keeps the live registers under the 256 of two waves per SIMD.
 //
 // Scores: S^T = K . Q^T as two v_mfma_f32_32x32x16 blocks (32 keys x 32
 // rows): each lane holds the scores of ONE row (lane % 32) for 16 keys per
@@ -37,6 +38,7 @@
 // P.V path never branches.
 #include <climits>
 #include <cmath>
+#include <type_traits>
 
 #include <hip/hip_ext.h>
 
@@ -52,7 +54,8 @@ constexpr int kRows = kWaves * 32;                   // rows per workgroup
 constexpr int kTileBytes = kTileKeys * kDim * 2;     // one K (or V) tile: 16 KiB
 constexpr int kTablePages = 2048;                    // block ids held in LDS at a time
 constexpr int kChunkTiles = kTablePages / 4;
-constexpr size_t kLdsBytes = 4 * kTileBytes + kTablePages * 4 + 16 * 4;  // K, V double buffers
+constexpr int kDummyBytes = 1024;                    // target of loads that are switched off
+constexpr size_t kLdsBytes = 4 * kTileBytes + kTablePages * 4 + 16 * 4 + kDummyBytes;  // K, V double buffers
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -73,6 +76,11 @@ template <> struct Mma32<bf16_t> {
   }
   __device__ static float2v unpack2(uint32_t w) {
     return float2v{__uint_as_float(w << 16), __uint_as_float(w & 0xFFFF0000u)};
+  }
+  // acc + the two bf16 values of w.
+  __device__ static float dot2_ones(uint32_t w, float acc) {
+    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
   }
 };
 
@@ -142,6 +150,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   uint8_t* const vbuf = smem + 2 * kTileBytes;  // V stages 0, 1
   int32_t* const page_tbl = reinterpret_cast<int32_t*>(smem + 4 * kTileBytes);
   int32_t* const red = page_tbl + kTablePages;
+  uint8_t* const dummy = reinterpret_cast<uint8_t*>(red + 16);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -153,21 +162,17 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   const int tpb = 1 << lg_tok;  // tokens per workgroup
   const int64_t R = a.num_requests;
   const int64_t nblk = a.num_tokens / tpb + R;
+  // Consecutive workgroups take the KV heads of one work item (so each XCD
+  // keeps reading the same head); items come heaviest first.
   const int h = static_cast<int>(blockIdx.x % Hkv);
-  // Late blocks of late requests first: they see the most keys.
-  const int64_t j = nblk - 1 - static_cast<int64_t>(blockIdx.x / Hkv);
-
-  // Request owning block slot j. Request r's blocks occupy slots
-  // [qsl[r] / T + r, qsl[r] / T + r + ceil(n_r / T)), which never overlap.
-  int64_t rl = 0, rh = R - 1;
-  while (rl < rh) {
-    const int64_t mid = (rl + rh + 1) >> 1;
-    if (a.qsl[mid] / tpb + mid <= j) rl = mid; else rh = mid - 1;
-  }
-  const int64_t r = rl;
+  const int64_t slot = static_cast<int64_t>(blockIdx.x / Hkv);
+  if (slot >= nblk) return;
+  const int2 item = a.items[slot];
+  if (item.x < 0 || item.x >= R) return;
+  const int64_t r = item.x;
   const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
   if (qs < 0 || qe > a.num_tokens || qe - qs <= 1) return;
-  const int64_t b = j - (qs / tpb + r);
+  const int64_t b = item.y;
   const int64_t t0 = qs + b * tpb;
   if (b < 0 || t0 >= qe) return;
   const int64_t t1 = t0 + tpb < qe ? t0 + tpb : qe;
@@ -252,7 +257,18 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   }
   const uint32_t kaddr = lds_address(kbuf);
   const uint32_t vaddr = lds_address(vbuf);
+  const uint32_t daddr = lds_address(dummy);
   const uint32_t bs32 = static_cast<uint32_t>(a.block_size);
+  // Byte offsets within a 16-row page segment of the page loads: instruction
+  // i covers rows 4 i .. 4 i + 3; lane l lands at row 4 i + l / 16, physical
+  // chunk l % 16, so it fetches the logical chunk that the swizzle puts there.
+  uint32_t dma_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rip = 4 * i + (lane >> 4);
+    dma_off[i] = static_cast<uint32_t>(2 * (rip * a.c_s[2] + 8 * ((lane & 15) ^ tile_swizzle(rip))));
+  }
+  const char* const cache_bytes = static_cast<const char*>(a.cache);
 
   for (int32_t c0 = 0; c0 < ntiles; c0 += kChunkTiles) {
     const int32_t nt = ntiles - c0 < kChunkTiles ? ntiles - c0 : kChunkTiles;
@@ -264,39 +280,18 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     }
     __syncthreads();
 
-    // Wave w moves page w of tile tl into LDS: instruction i covers page rows
-    // 4 i .. 4 i + 3; lane l lands at row 4 i + l / 16, physical chunk l % 16,
-    // so it fetches the logical chunk that the swizzle puts there.
-    auto page_src = [&](int32_t tl, int32_t id) {
+    // Wave w moves page w of each tile into LDS (K and V), four 1 KiB
+    // instructions each. Byte address of the K page segment of tile tl:
+    auto page_base = [&](int32_t tl, int32_t id) {
       const uint32_t pos = static_cast<uint32_t>(base + kTileKeys * (c0 + tl) + 16 * wave);
       const int64_t row0 = pos % bs32;
-      return cache + static_cast<int64_t>(id) * a.c_s[1] + row0 * a.c_s[2] + head_elems;
+      return cache_bytes + 2 * (static_cast<int64_t>(id) * a.c_s[1] + row0 * a.c_s[2] + head_elems);
     };
-    auto issue_k = [&](int32_t tl, int stage, int32_t id) {
-      if (id < 0) return;  // an unmapped page's keys are masked
-      const uint16_t* page = page_src(tl, id);
-      const uint32_t dst = kaddr + stage * kTileBytes + wave * 4096;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rip = 4 * i + (lane >> 4);
-        lds_dma_load16(page + rip * a.c_s[2] + 8 * ((lane & 15) ^ tile_swizzle(rip)), dst + i * 1024);
-      }
-    };
-    auto issue_v = [&](int32_t tl, int stage, int32_t id) {
+    // Unmapped page (or beyond the last visible key): its V rows are zeroed.
+    auto zero_v = [&](int stage) {
       uint8_t* slot = vbuf + stage * kTileBytes + wave * 4096;
-      if (id < 0) {
-        // Unmapped (or beyond the last visible key): zero rows.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(slot + i * 1024 + 16 * lane) = uint4{0, 0, 0, 0};
-        return;
-      }
-      const uint16_t* page = page_src(tl, id) + a.c_s[0];
-      const uint32_t dst = vaddr + stage * kTileBytes + wave * 4096;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rip = 4 * i + (lane >> 4);
-        lds_dma_load16(page + rip * a.c_s[2] + 8 * ((lane & 15) ^ tile_swizzle(rip)), dst + i * 1024);
-      }
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(slot + i * 1024 + 16 * lane) = uint4{0, 0, 0, 0};
     };
     // After the loads landed: zero the V rows of this wave's page that lie
     // outside [kmin, kmax] (they may hold stale or non-finite data).
@@ -327,137 +322,173 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
       const int32_t v = wave == 0 ? ids.x : wave == 1 ? ids.y : wave == 2 ? ids.z : ids.w;
       return __builtin_amdgcn_readfirstlane(v);
     };
-    // cur_ids: tile tl; nxt_ids: tile tl + 1 (read one iteration ahead).
-    int4 cur_ids = tile_ids(0), nxt_ids = tile_ids(1);
-    auto step = [&](int32_t tl) {
-      const int stage = tl & 1;
-      if (tl + 1 < nt) {
-        const int32_t id = own_id(nxt_ids);
-        issue_k(tl + 1, stage ^ 1, id);
-        issue_v(tl + 1, stage ^ 1, id);
-      }
+    // Wave-uniform page facts of tile tl (valid-page mask) and tile tl + 1
+    // (this wave's block id, mask), read from LDS one iteration ahead.
+    uint32_t cur_mask = page_mask(tile_ids(0));
+    int32_t nxt_own;
+    uint32_t nxt_mask;
+    {
+      const int4 ids = tile_ids(1);
+      nxt_own = own_id(ids);
+      nxt_mask = page_mask(ids);
+    }
+    // The stage is a compile-time constant (the loop below is unrolled by
+    // two), so LDS offsets fold into the instructions' offset fields.
+    auto step = [&](int32_t tl, auto stage_c) {
+      constexpr int stage = decltype(stage_c)::value;
+      // Loads of tile tl + 1 into the other stage, issued between the S
+      // MFMAs below so that the address unit drains while the matrix cores
+      // work (a burst of loads stalls the issuing wave).
+      const int32_t nid = nxt_own;
+      // A load that is switched off (no next tile, or an unmapped page)
+      // still reads a mapped page but lands in the dummy region, so the
+      // sequence has no branches.
+      const bool dma_on = tl + 1 < nt && nid >= 0;
+      if (tl + 1 < nt && nid < 0) zero_v(stage ^ 1);
+      const char* const kp = page_base(tl + 1, nid >= 0 ? nid : 0);
+      const char* const vp = kp + 2 * a.c_s[0];
+      const uint32_t kdst = dma_on ? kaddr + (stage ^ 1) * kTileBytes + wave * 4096 : daddr;
+      const uint32_t vdst = dma_on ? vaddr + (stage ^ 1) * kTileBytes + wave * 4096 : daddr;
       const int4 fut_ids = tile_ids(tl + 2);
-      const int32_t k0 = base + kTileKeys * (c0 + tl);
-      const uint32_t pv = page_mask(cur_ids);
-      const bool edge = k0 < w_lo_max || k0 + kTileKeys - 1 > w_hi_min || pv != 0xFu;
       const uint8_t* kt = kbuf + stage * kTileBytes;
       const uint8_t* vt = vbuf + stage * kTileBytes;
 
-      short8_t kf[2][8];
-#pragma unroll
-      for (int st = 0; st < 8; ++st) kf[0][st] = *reinterpret_cast<const short8_t*>(kt + koff[st]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int st = 0; st < 8; ++st) kf[1][st] = *reinterpret_cast<const short8_t*>(kt + 8192 + koff[st]);
-      float16v s_cur[2];
-      s_cur[0] = float16v{};
-      s_cur[1] = float16v{};
-#pragma unroll
-      for (int st = 0; st < 8; ++st) s_cur[0] = Mma32<T>::mma(kf[0][st], qv[st], s_cur[0]);
-#pragma unroll
-      for (int st = 0; st < 8; ++st) s_cur[1] = Mma32<T>::mma(kf[1][st], qv[st], s_cur[1]);
-      __builtin_amdgcn_sched_barrier(0);
-      // V operands of the first two 16-key steps, in flight during the softmax.
-      short4v vf[4][8];
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int x = 0; x < 8; ++x) vf[q][x] = lds_read_tr16(vt + 256 * (16 * q) + voff[x]);
-      __builtin_amdgcn_sched_barrier(0);
-
-      // s_cur[bb][i] = score of key 32 bb + 8 (i / 4) + 4 hh + i % 4, row n.
-      if (edge) {
-        // The empty asm keeps the compiler from if-converting the masking
-        // into every tile: interior tiles skip it entirely.
-        asm volatile("");
-        const int32_t rlo = lo_n - k0, rhi = hi_n - k0;
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kk = 32 * bb + 8 * (i >> 2) + 4 * hh + (i & 3);
-            const bool page_ok = (pv >> (2 * bb + (i >> 3))) & 1u;
-            const bool vis = page_ok && kk >= rlo && kk <= rhi;
-            s_cur[bb][i] = vis ? s_cur[bb][i] : -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[bb][i]);
-      mx = max_with_partner(mx);
-      const float mx_c = mx * cs;
-      const bool grow = mx_c > m_c + 8.f;
-      if (__ballot(grow)) {
-        const float m_new = grow ? mx_c : m_c;
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
-        l *= alpha;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
-        m_c = m_new;
-      }
-      const float m_use = m_c == -INFINITY ? 0.f : m_c;
-
-      short8_t pb[4], pbl[4];
+      // Two halves of 32 keys, each a full online-softmax update.
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb) {
-        float p[16];
+        const int32_t k0 = base + kTileKeys * (c0 + tl) + 32 * bb;
+        const uint32_t pv = (cur_mask >> (2 * bb)) & 3u;
+        const bool edge = k0 < w_lo_max || k0 + 31 > w_hi_min || pv != 3u;
+        short8_t kf[8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[bb][i], cs, -m_use));
-          l += p[i];
-        }
+        for (int st = 0; st < 8; ++st) kf[st] = *reinterpret_cast<const short8_t*>(kt + 8192 * bb + koff[st]);
+        __builtin_amdgcn_sched_barrier(0);
+        float16v s_cur = float16v{};
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          // P^T B operand: keys 32 bb + 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
-          uint32_t ph[4], pl[4];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
-            if constexpr (PSPLIT) {
-              const float2v back = Mma32<T>::unpack2(ph[w]);
-              pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
-            }
+        for (int st = 0; st < 8; ++st) {
+          s_cur = Mma32<T>::mma(kf[st], qv[st], s_cur);
+          if (st & 1) {
+            // Loads of tile tl + 1: K pages during the first half, V pages
+            // during the second.
+            const int i = st >> 1;
+            __builtin_amdgcn_sched_barrier(0);
+            if (bb == 0) lds_dma_load16_sbase(kp, dma_off[i], kdst + (dma_on ? i * 1024 : 0));
+            else lds_dma_load16_sbase(vp, dma_off[i], vdst + (dma_on ? i * 1024 : 0));
+            __builtin_amdgcn_sched_barrier(0);
           }
-          pb[2 * bb + s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
-          if constexpr (PSPLIT) pbl[2 * bb + s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
         }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // O^T += V^T . P^T over the four 16-key steps q; the V operands of
-      // step q + 2 are read while step q multiplies.
+        // V operands of the half's first 16-key step, in flight during the
+        // softmax (double-buffered: the second step is read during the first).
+        short4v vf[2][8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q + 2 < 4) {
+        for (int x = 0; x < 8; ++x) vf[0][x] = lds_read_tr16(vt + 8192 * bb + voff[x]);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // s_cur[i] = score of key k0 + 8 (i / 4) + 4 hh + i % 4, row n.
+        if (edge) {
+          // The empty asm keeps the compiler from if-converting the masking
+          // into every step: interior steps skip it entirely.
+          asm volatile("");
+          const int32_t rlo = lo_n - k0, rhi = hi_n - k0;
 #pragma unroll
-          for (int x = 0; x < 8; ++x) vf[q + 2][x] = lds_read_tr16(vt + 256 * (16 * (q + 2)) + voff[x]);
+          for (int i = 0; i < 16; ++i) {
+            const int kk = 8 * (i >> 2) + 4 * hh + (i & 3);
+            const bool page_ok = (pv >> (i >> 3)) & 1u;
+            const bool vis = page_ok && kk >= rlo && kk <= rhi;
+            s_cur[i] = vis ? s_cur[i] : -INFINITY;
+          }
         }
+        float mx = -INFINITY;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const short4v lo4 = vf[q][c], hi4 = vf[q][4 + c];
-          const short8_t av = short8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          oacc[c] = Mma32<T>::mma(av, pb[q], oacc[c]);
-          if constexpr (PSPLIT) oacc[c] = Mma32<T>::mma(av, pbl[q], oacc[c]);
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[i]);
+        mx = max_with_partner(mx);
+        const float mx_c = mx * cs;
+        const bool grow = mx_c > m_c + 8.f;
+        if (__ballot(grow)) {
+          const float m_new = grow ? mx_c : m_c;
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
+          l *= alpha;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+          m_c = m_new;
+        }
+        const float m_use = m_c == -INFINITY ? 0.f : m_c;
+
+        short8_t pb[2], pbl[2];
+        {
+          float p[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[i], cs, -m_use));
+            if constexpr (PSPLIT) l += p[i];
+          }
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            // P^T B operand: keys 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
+            uint32_t ph[4], pl[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
+              // bf16: the row sum adds the rounded probabilities that the
+              // P.V product uses, two per instruction.
+              if constexpr (!PSPLIT) l = Mma32<T>::dot2_ones(ph[w], l);
+              if constexpr (PSPLIT) {
+                const float2v back = Mma32<T>::unpack2(ph[w]);
+                pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
+              }
+            }
+            pb[s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
+            if constexpr (PSPLIT) pbl[s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
+        // O^T += V^T . P^T over the half's two 16-key steps q.
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (q == 0) {
+#pragma unroll
+            for (int x = 0; x < 8; ++x) vf[1][x] = lds_read_tr16(vt + 8192 * bb + 256 * 16 + voff[x]);
+          }
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const short4v lo4 = vf[q][c], hi4 = vf[q][4 + c];
+            const short8_t av = short8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            oacc[c] = Mma32<T>::mma(av, pb[q], oacc[c]);
+            if constexpr (PSPLIT) oacc[c] = Mma32<T>::mma(av, pbl[q], oacc[c]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
       wait_vmcnt<0>();
       if (tl + 1 < nt) fix_v(tl + 1, stage ^ 1);
       __syncthreads();
-      cur_ids = nxt_ids;
-      nxt_ids = fut_ids;
+      cur_mask = nxt_mask;
+      nxt_own = own_id(fut_ids);
+      nxt_mask = page_mask(fut_ids);
     };
 
     {
-      const int32_t id = own_id(cur_ids);
-      issue_k(0, 0, id);
-      issue_v(0, 0, id);
+      const int32_t id = own_id(tile_ids(0));
+      const char* kp = page_base(0, id >= 0 ? id : 0);
+      if (id < 0) {
+        zero_v(0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lds_dma_load16_sbase(kp, dma_off[i], kaddr + wave * 4096 + i * 1024);
+          lds_dma_load16_sbase(kp + 2 * a.c_s[0], dma_off[i], vaddr + wave * 4096 + i * 1024);
+        }
+      }
     }
     wait_vmcnt<0>();
     fix_v(0, 0);
     __syncthreads();
-    for (int32_t tl = 0; tl < nt; ++tl) step(tl);
+    int32_t tl = 0;
+    for (; tl + 1 < nt; tl += 2) {
+      step(tl, std::integral_constant<int, 0>{});
+      step(tl + 1, std::integral_constant<int, 1>{});
+    }
+    if (tl < nt) step(tl, std::integral_constant<int, 0>{});
   }
 
   const float lt = sum_with_partner(l);
@@ -475,6 +506,106 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     }
 }
 
+// ---- prefill work list ------------------------------------------------------
+//
+// Request r's query blocks of T tokens occupy work-list slots
+// [qsl[r] / T + r, qsl[r] / T + r + ceil(n_r / T)), which never overlap and
+// stay below N / T + R. One workgroup lists every (request, block) item of
+// the multi-query requests, sorted by the number of 64-key tiles it visits,
+// heaviest first, so that the hardware's in-order dispatch of the prefill
+// grid approximates longest-processing-time-first scheduling. Empty slots
+// (single-query requests) go last as request -1. Items within a cost
+// bucket come in any order; every item writes only its own output rows.
+constexpr int kItemThreads = 1024;
+constexpr int kItemSlots = 8192;    // larger batches keep slot order (late slots first)
+constexpr int kCostBuckets = 2048;  // tiles per item, clamped
+static_assert(kCostBuckets == 2 * kItemThreads, "the bucket scan gives each thread two buckets");
+
+__global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a, int32_t lg_tok) {
+  __shared__ int32_t owner[kItemSlots];
+  __shared__ uint16_t bucket_of[kItemSlots];
+  __shared__ int32_t start[kCostBuckets];
+  __shared__ int32_t wave_sums[kItemThreads / 64];
+  __shared__ int32_t total;
+  const int tid = threadIdx.x;
+  const int64_t tpb = int64_t{1} << lg_tok;
+  const int64_t R = a.num_requests;
+  const int64_t nslots = a.num_tokens / tpb + R;
+  if (nslots > kItemSlots) {
+    for (int64_t j = tid; j < nslots; j += kItemThreads) {
+      int64_t rl = 0, rh = R - 1;
+      while (rl < rh) {
+        const int64_t mid = (rl + rh + 1) >> 1;
+        if (a.qsl[mid] / tpb + mid <= j) rl = mid; else rh = mid - 1;
+      }
+      const int64_t qs = a.qsl[rl], qe = a.qsl[rl + 1];
+      const int64_t b = j - (qs / tpb + rl);
+      const bool ok = qs >= 0 && qe <= a.num_tokens && qe - qs > 1 && b >= 0 && qs + b * tpb < qe;
+      a.items[nslots - 1 - j] = ok ? int2{static_cast<int>(rl), static_cast<int>(b)} : int2{-1, -1};
+    }
+    return;
+  }
+  for (int j = tid; j < nslots; j += kItemThreads) owner[j] = -1;
+  for (int k = tid; k < kCostBuckets; k += kItemThreads) start[k] = 0;
+  __syncthreads();
+  for (int64_t r = tid; r < R; r += kItemThreads) {
+    const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
+    if (qs < 0 || qe > a.num_tokens || qe - qs <= 1) continue;
+    const int64_t first = qs / tpb + r;
+    const int64_t nb = (qe - qs + tpb - 1) / tpb;
+    for (int64_t b = 0; b < nb && first + b < nslots; ++b) owner[first + b] = static_cast<int32_t>(r);
+  }
+  __syncthreads();
+  // Cost of an item: 64-key tiles between its first row's first visible key
+  // and its last row's last one.
+  for (int j = tid; j < nslots; j += kItemThreads) {
+    const int32_t r = owner[j];
+    if (r < 0) continue;
+    const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
+    const int64_t t0 = qs + (j - (qs / tpb + r)) * tpb;
+    const int64_t t1 = (t0 + tpb < qe ? t0 + tpb : qe) - 1;
+    int64_t lo0, hi0, lo1, hi1;
+    visible_range(a, r, qs, t0, lo0, hi0);
+    visible_range(a, r, qs, t1, lo1, hi1);
+    const int64_t tiles = hi1 >= lo0 ? (hi1 - lo0 + 64) / 64 : 0;
+    const int bucket = static_cast<int>(tiles < kCostBuckets - 1 ? tiles : kCostBuckets - 1);
+    bucket_of[j] = static_cast<uint16_t>(bucket);
+    atomicAdd(&start[bucket], 1);
+  }
+  __syncthreads();
+  // start[k] = number of items in buckets above k (exclusive scan, heaviest
+  // first). Thread t owns buckets K - 1 - 2 t and K - 2 - 2 t.
+  {
+    const int k0 = kCostBuckets - 1 - 2 * tid;
+    const int v0 = start[k0], v1 = start[k0 - 1];
+    const int own = v0 + v1;
+    int incl = own;
+    const int lane = tid & 63, w = tid >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wave_sums[w] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int i = 0; i < w; ++i) before += wave_sums[i];
+    const int excl = before + incl - own;
+    if (tid == kItemThreads - 1) total = excl + own;
+    __syncthreads();
+    start[k0] = excl;
+    start[k0 - 1] = excl + v0;
+  }
+  __syncthreads();
+  for (int j = tid; j < nslots; j += kItemThreads) {
+    const int32_t r = owner[j];
+    if (r < 0) continue;
+    const int pos = atomicAdd(&start[bucket_of[j]], 1);
+    a.items[pos] = int2{r, static_cast<int>(j - (a.qsl[r] / tpb + r))};
+  }
+  for (int64_t j = total + tid; j < nslots; j += kItemThreads) a.items[j] = int2{-1, -1};
+}
+
 template <typename T, bool PSPLIT>
 int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   int lg_tok = 0;
@@ -483,6 +614,9 @@ int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEven
   const int64_t blocks = nblk * a.num_kv_heads;
   if (blocks <= 0) return MVLLM_OK;
   if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "prefill grid too large");
+  if (!a.items) return fail(MVLLM_ERR_INVALID, "prefill work list is missing");
+  prefill_items_kernel<<<1, kItemThreads, 0, s>>>(a, lg_tok);
+  MVLLM_LAUNCH_CHECK("prefill_items_kernel");
   static bool raised = false;  // per instantiation; the attribute is process-wide
   if (!raised) {
     MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<T, PSPLIT>),

@@ -165,6 +165,18 @@ __device__ __forceinline__ void lds_dma_load16_stream(const void* global_ptr, ui
       : "memory", "m0");
 }
 
+// lds_dma_load16 with a wave-uniform 64-bit base in SGPRs and a per-lane
+// 32-bit byte offset, which saves the 64-bit vector address arithmetic.
+__device__ __forceinline__ void lds_dma_load16_sbase(const void* base, uint32_t offset, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %2"
+      :
+      : "v"(offset), "s"(__builtin_amdgcn_readfirstlane(lds_base)), "s"(base)
+      : "memory", "m0");
+}
+
 // s_waitcnt with vmcnt <= N (N < 64), other counters unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
