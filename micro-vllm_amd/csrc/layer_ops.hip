@@ -94,6 +94,66 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(NormArgs a) 
   }
 }
 
+// Vectorised form: one wave per row, lane l holds dims 8 (l + 64 c) .. +8
+// for chunk c < CHUNKS (dim <= 512 CHUNKS), 16-byte loads and stores. Needs
+// dim % 8 == 0 and 16-byte aligned rows; the kernel above covers the rest.
+template <typename T, int CHUNKS>
+__global__ __launch_bounds__(256) void add_rms_norm_rows_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const uint16_t* x = a.x + row * a.x_stride;
+  uint16_t* res = a.residual ? a.residual + row * a.res_stride : nullptr;
+  float h[CHUNKS][8];
+  float sq = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int d = 8 * (lane + 64 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[c][e] = 0.f;
+    if (d < a.dim) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(x + d);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[c][e] = Act<T>::load((xw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      if (res) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(res + d);
+        const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          h[c][e] = Act<T>::round(Act<T>::load((rw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) + h[c][e]);
+          if (e & 1) ow[e >> 1] |= static_cast<uint32_t>(Act<T>::store(h[c][e])) << 16;
+          else ow[e >> 1] = Act<T>::store(h[c][e]);
+        }
+        *reinterpret_cast<uint4*>(res + d) = uint4{ow[0], ow[1], ow[2], ow[3]};
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(h[c][e], h[c][e], sq);
+    }
+  }
+  sq = wave_sum(sq);
+  const float inv = 1.f / sqrtf(sq / static_cast<float>(a.dim) + a.eps);
+  uint16_t* out = a.out + row * a.out_stride;
+#pragma unroll
+  for (int c = 0; c < CHUNKS; ++c) {
+    const int d = 8 * (lane + 64 * c);
+    if (d < a.dim) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(a.weight + d);
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float normed = Act<T>::round(h[c][e] * inv);
+        const uint32_t o = Act<T>::store(Act<T>::load((ww[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) * normed);
+        if (e & 1) ow[e >> 1] |= o << 16;
+        else ow[e >> 1] = o;
+      }
+      *reinterpret_cast<uint4*>(out + d) = uint4{ow[0], ow[1], ow[2], ow[3]};
+    }
+  }
+}
+
 // --------------------------------------------------- qk_norm_rope_kv_write
 
 struct QkArgs {
@@ -166,6 +226,88 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkArgs a) {
   *reinterpret_cast<uint32_t*>(dst + 2 * lane) = result;
 }
 
+// Vectorised form: one wave per token, its rows in passes of four. Lanes
+// 16 g .. 16 g + 15 hold row 4 p + g; lane j of a row holds dims 8 j .. +8
+// (16-byte loads and stores), whose rotate-half partners sit in lane j ^ 8.
+// The token's cos/sin values and cache slot are loaded once. Needs 16-byte
+// aligned rows; the kernel above covers the rest.
+template <typename T>
+__global__ __launch_bounds__(256) void qk_norm_rope_token_kernel(QkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= a.num_tokens) return;
+  const int g = lane >> 4, j = lane & 15;
+  const int rows = a.num_q_heads + 2 * a.num_kv_heads;
+  float cv[8], sv[8];
+  if (a.cos) {
+    const float4* cp = reinterpret_cast<const float4*>(a.cos + t * 128 + 8 * j);
+    const float4* sp = reinterpret_cast<const float4*>(a.sin + t * 128 + 8 * j);
+    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    cv[0] = c0.x; cv[1] = c0.y; cv[2] = c0.z; cv[3] = c0.w; cv[4] = c1.x; cv[5] = c1.y; cv[6] = c1.z; cv[7] = c1.w;
+    sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+  }
+  const int64_t slot = a.slots[t];
+  const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  const int64_t block = slot_ok ? slot / a.block_size : 0;
+  uint16_t* const kv_row = a.cache + block * a.c_s[1] + (slot_ok ? slot - block * a.block_size : 0) * a.c_s[2];
+  for (int p = 0; p < rows; p += 4) {
+    const int row = p + g;
+    const bool live = row < rows;
+    const int rr = live ? row : rows - 1;  // idle groups repeat a valid row and store nothing
+    const bool is_q = rr < a.num_q_heads;
+    const bool is_v = rr >= a.num_q_heads + a.num_kv_heads;
+    const int head = is_q ? rr : is_v ? rr - a.num_q_heads - a.num_kv_heads : rr - a.num_q_heads;
+    const uint16_t* src = is_q ? a.q + t * a.q_s0 + head * a.q_s1
+                        : is_v ? a.v + t * a.v_s0 + head * a.v_s1
+                               : a.k + t * a.k_s0 + head * a.k_s1;
+    const uint4 raw = *reinterpret_cast<const uint4*>(src + 8 * j);
+    uint4 result = raw;
+    if (!is_v) {
+      const uint32_t rw[4] = {raw.x, raw.y, raw.z, raw.w};
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = Act<T>::load((rw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      const uint16_t* w = is_q ? a.q_weight : a.k_weight;
+      if (w) {
+        float sq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(x[e], x[e], sq);
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) sq += __shfl_xor(sq, m, 64);  // within the row's 16 lanes
+        const float inv = 1.f / sqrtf(sq / 128.f + a.eps);
+        const uint4 wv = *reinterpret_cast<const uint4*>(w + 8 * j);
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          x[e] = Act<T>::round(Act<T>::load((ww[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) * Act<T>::round(x[e] * inv));
+      }
+      if (a.cos) {
+        // rotate_half: dims < 64 take -x[d + 64], dims >= 64 take x[d - 64].
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = __shfl_xor(x[e], 8, 64);
+          r[e] = j < 8 ? -pe : pe;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = __fadd_rn(__fmul_rn(x[e], cv[e]), __fmul_rn(r[e], sv[e]));
+      }
+      uint32_t ow[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ow[e] = static_cast<uint32_t>(Act<T>::store(x[2 * e])) | (static_cast<uint32_t>(Act<T>::store(x[2 * e + 1])) << 16);
+      result = uint4{ow[0], ow[1], ow[2], ow[3]};
+    }
+    if (!live) continue;
+    if (is_q) {
+      *reinterpret_cast<uint4*>(a.q_out + (t * a.num_q_heads + head) * 128 + 8 * j) = result;
+    } else if (slot_ok) {
+      uint16_t* dst = kv_row + (is_v ? a.c_s[0] : 0) + head * a.c_s[3];
+      *reinterpret_cast<uint4*>(dst + 8 * j) = result;
+    }
+  }
+}
+
 // --------------------------------------------------------------- silu_mul
 
 struct SiluArgs {
@@ -199,6 +341,21 @@ bool half_dtype(int32_t d) { return d == MVLLM_DTYPE_BF16 || d == MVLLM_DTYPE_F1
 
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
+bool mult8(int64_t v) { return (v & 7) == 0; }
+
+template <typename T>
+int launch_add_rms_norm_rows(const NormArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+  const int chunks = (a.dim + 511) / 512;
+  if (chunks <= 1) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 1>), grid, dim3(256), 0, s, a);
+  else if (chunks <= 2) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 2>), grid, dim3(256), 0, s, a);
+  else if (chunks <= 4) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 4>), grid, dim3(256), 0, s, a);
+  else if (chunks <= 8) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 8>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 16>), grid, dim3(256), 0, s, a);
+  MVLLM_LAUNCH_CHECK("add_rms_norm_rows_kernel");
+  return MVLLM_OK;
+}
+
 }  // namespace
 }  // namespace mvllm
 
@@ -219,6 +376,10 @@ extern "C" int mvllm_add_rms_norm(const void* x, int64_t x_stride, void* residua
              static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), x_stride, residual_stride,
              out_stride, rows, static_cast<int32_t>(dim), eps};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = mult8(dim) && mult8(x_stride) && mult8(out_stride) && aligned16(x) && aligned16(weight) &&
+                   aligned16(out) && (!residual || (mult8(residual_stride) && aligned16(residual)));
+  if (vec && dtype == MVLLM_DTYPE_BF16) return launch_add_rms_norm_rows<bf16_t>(a, s);
+  if (vec) return launch_add_rms_norm_rows<f16_t>(a, s);
   if (dtype == MVLLM_DTYPE_BF16)
     hipLaunchKernelGGL(add_rms_norm_kernel<bf16_t>, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0, s, a);
   else
@@ -275,10 +436,25 @@ extern "C" int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query, const mvl
   a.num_q_heads = static_cast<int32_t>(query->size[1]);
   a.num_kv_heads = static_cast<int32_t>(key->size[1]);
   a.eps = eps;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = aligned16(query->data) && aligned16(key->data) && aligned16(value->data) && aligned16(q_out) &&
+                   aligned16(cache->data) && mult8(a.q_s0) && mult8(a.q_s1) && mult8(a.k_s0) && mult8(a.k_s1) &&
+                   mult8(a.v_s0) && mult8(a.v_s1) && mult8(a.c_s[0]) && mult8(a.c_s[1]) && mult8(a.c_s[2]) &&
+                   mult8(a.c_s[3]) && (!q_weight || (aligned16(q_weight) && aligned16(k_weight))) &&
+                   (!cos_table || (aligned16(cos_table) && aligned16(sin_table)));
+  if (vec) {
+    const int64_t blocks = (N + 3) / 4;
+    if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: grid too large");
+    if (dtype == MVLLM_DTYPE_BF16)
+      hipLaunchKernelGGL(qk_norm_rope_token_kernel<bf16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(qk_norm_rope_token_kernel<f16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    MVLLM_LAUNCH_CHECK("qk_norm_rope_token_kernel");
+    return MVLLM_OK;
+  }
   const int64_t items = N * (query->size[1] + 2 * key->size[1]);
   const int64_t blocks = (items + 3) / 4;
   if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: grid too large");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (dtype == MVLLM_DTYPE_BF16)
     hipLaunchKernelGGL(qk_norm_rope_kernel<bf16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
   else
