@@ -221,6 +221,7 @@ def run_e2e(args, device) -> dict:
         max_num_seqs=256,
         max_model_len=max_model_len,
         decode_graphs=not args.e2e_eager,
+        pipeline=not args.e2e_eager and not args.e2e_sync,
     )
     if engine.graphs is not None:
         # Capture every bucket before timing (the reference captures at start-up, model_runner.py:344-497).
@@ -249,12 +250,18 @@ def run_e2e(args, device) -> dict:
                 f"requests with random prompts U[64,1024], {args.e2e_max_tokens} greedy tokens each, "
                 "max_num_batched_tokens 8192, max_num_seqs 256, block 16, "
                 + ("eager" if args.e2e_eager else "decode steps as HIP graphs (buckets 1..256)")
+                + ("" if args.e2e_eager or args.e2e_sync else ", host one step ahead (pipelined)")
                 + ("; torch layers" if args.e2e_unfused else "; fused HIP layer kernels")
             ),
             "parameters": model.parameter_count(),
             "prompt_tokens": result.prompt_tokens,
             "output_tokens": result.output_tokens,
             "step_seconds": round(result.step_seconds, 4),
+            "timing": (
+                "synchronized steps summed"
+                if args.e2e_eager or args.e2e_sync
+                else "wall time of the generation loop (steps overlap)"
+            ),
             "decode_steps": result.decode_steps,
             "decode_step_ms": round(result.decode_seconds / max(result.decode_steps, 1) * 1e3, 3),
             "other_steps": result.steps - result.decode_steps,
@@ -280,6 +287,11 @@ def main() -> int:
     parser.add_argument("--e2e-eager", action="store_true", help="run qwen3_e2e decode steps eagerly (no HIP graphs)")
     parser.add_argument(
         "--e2e-unfused", action="store_true", help="qwen3_e2e with the torch layers instead of the fused HIP layer kernels"
+    )
+    parser.add_argument(
+        "--e2e-sync",
+        action="store_true",
+        help="qwen3_e2e graph steps one at a time (no host/GPU overlap), each step timed synchronized",
     )
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=10)

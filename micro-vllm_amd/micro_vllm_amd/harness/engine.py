@@ -28,6 +28,16 @@ kernels rewrite the bucket's static input buffers (padded the way
 model_runner.py:78-122 pads them: no tokens past the real ones, slot -1,
 null block ids) and the captured forward, greedy argmax included, is
 replayed.
+
+With `pipeline=True` the host runs one graph step ahead of the GPU: it
+schedules and launches step k + 1 before reading step k's tokens back, so the
+scheduling, packing and bookkeeping of one step overlap the previous step on
+the GPU. Scheduling needs only token counts (a request finishes after
+`max_tokens` outputs), so a token that is still on the GPU is carried as a
+placeholder, -(1 + r) for row r of the previous step's samples, which the
+captured graph replaces on the device with that step's sampled token. Before
+any step that does not run as a graph, the pending step is read back and the
+placeholders are filled in.
 """
 
 from __future__ import annotations
@@ -109,6 +119,7 @@ class GenerationEngine:
         max_num_seqs: int = 256,
         max_model_len: int = 8192,
         decode_graphs: bool = False,
+        pipeline: bool = False,
     ) -> None:
         c = model.config
         self.model = model
@@ -134,6 +145,9 @@ class GenerationEngine:
         self._requests: dict[str, Request] = {}
         self.preemptions = 0
         self.graphs = DecodeGraphs(self) if decode_graphs else None
+        if pipeline and self.graphs is None:
+            raise ValueError("pipeline=True needs decode_graphs=True")
+        self.pipeline = pipeline
 
     # ------------------------------------------------------------ requests
     def add_request(self, request: Request) -> None:
@@ -259,9 +273,11 @@ class GenerationEngine:
         return logits.argmax(dim=-1).tolist()
 
     def generate(self, requests: list[Request]) -> GenerationResult:
-        """Run every request to completion; time the synchronized steps
-        (schedule + execute + update, as the reference benchmark times
-        Engine.step, benchmarks/benchmark_engine.py:312-315)."""
+        """Run every request to completion. Synchronous mode times the
+        synchronized steps (schedule + execute + update, as the reference
+        benchmark times Engine.step, benchmarks/benchmark_engine.py:312-315);
+        pipelined mode overlaps steps, so it times the whole loop, and a
+        step's time is the wall time from its start to the next step's."""
 
         for request in requests:
             self.add_request(request)
@@ -269,18 +285,36 @@ class GenerationEngine:
         seconds = decode_seconds = 0.0
         device = self.model.device
         torch.cuda.synchronize(device)
+        pending: PendingStep | None = None
+        loop_start = time.perf_counter()
         while self.has_unfinished_requests():
             start = time.perf_counter()
             plan = self.schedule()
-            sampled = self.execute(plan)
-            torch.cuda.synchronize(device)
-            self._update(plan, sampled)
+            if self.pipeline and self.graphs.accepts(plan):
+                launched = self.graphs.launch(plan)
+                if pending is not None:
+                    self._resolve(pending)
+                self._update_pending(plan, launched)
+                pending = launched
+            else:
+                if pending is not None:
+                    self._resolve(pending)
+                    pending = None
+                    plan = self._refresh(plan)
+                sampled = self.execute(plan)
+                torch.cuda.synchronize(device)
+                self._update(plan, sampled)
             elapsed = time.perf_counter() - start
             seconds += elapsed
             steps += 1
             if all(s.num_scheduled_tokens == 1 for s in plan.scheduled_requests):
                 decode_steps += 1
                 decode_seconds += elapsed
+        if pending is not None:
+            self._resolve(pending)
+        if self.pipeline:
+            torch.cuda.synchronize(device)
+            seconds = time.perf_counter() - loop_start
         return GenerationResult(
             outputs={r.request_id: list(r.output_token_ids) for r in requests},
             steps=steps,
@@ -291,6 +325,48 @@ class GenerationEngine:
             decode_steps=decode_steps,
             decode_seconds=decode_seconds,
         )
+
+    # ------------------------------------------------------- pipelining
+    def _update_pending(self, plan: SchedulerOutput, step: "PendingStep") -> None:
+        """_update for a launched graph step whose tokens are still on the
+        GPU: every request gets a placeholder for its token."""
+
+        for row, item in enumerate(plan.scheduled_requests):
+            request = self._requests[item.request_id]
+            request.num_computed_tokens += 1
+            request.append_output(-(1 + row))
+            step.slots.append((request, len(request.output_token_ids) - 1))
+            if request.finished:
+                self._running.remove(request)
+                self._free(request)
+
+    def _resolve(self, step: "PendingStep") -> None:
+        """Replace a launched step's placeholders with its sampled tokens."""
+
+        step.event.synchronize()
+        values = step.host[: len(step.slots)].tolist()
+        for (request, index), token in zip(step.slots, values):
+            request.output_token_ids[index] = token
+            request.token_ids[len(request.prompt_token_ids) + index] = token
+
+    def _refresh(self, plan: SchedulerOutput) -> SchedulerOutput:
+        """The plan's input ids re-read after placeholders were resolved."""
+
+        items = []
+        for item in plan.scheduled_requests:
+            request = self._requests[item.request_id]
+            start = item.num_computed_tokens
+            items.append(
+                ScheduledRequest(
+                    request_id=item.request_id,
+                    input_token_ids=tuple(request.token_ids[start : start + item.num_scheduled_tokens]),
+                    num_computed_tokens=start,
+                    num_scheduled_tokens=item.num_scheduled_tokens,
+                    requires_sampling=item.requires_sampling,
+                    block_tables=item.block_tables,
+                )
+            )
+        return SchedulerOutput(tuple(items), plan.preempted_request_ids)
 
 
 class DecodeGraphs:
@@ -304,6 +380,12 @@ class DecodeGraphs:
         self.max_batch = self.BUCKETS[-1]
         self.pool = torch.cuda.graph_pool_handle()
         self.entries: dict[int, DecodeGraph] = {}
+        device = engine.model.device
+        # The sampled tokens of the latest graph step, read by the next one
+        # through placeholders (pipelined mode).
+        self.last_tokens = torch.zeros(self.max_batch, dtype=torch.int64, device=device)
+        self._host = [torch.empty(self.max_batch, dtype=torch.int64, pin_memory=True) for _ in range(2)]
+        self._flip = 0
 
     def accepts(self, plan: SchedulerOutput) -> bool:
         items = plan.scheduled_requests
@@ -330,9 +412,14 @@ class DecodeGraphs:
         """The decode step on a bucket's buffers: logits and greedy token of every row."""
 
         model = self.engine.model
-        hidden = model.forward(buffers.input_ids, buffers.positions, self.engine.kv_caches, buffers.group_metadata[0])
+        ids = buffers.input_ids
+        # Placeholder -(1 + r): the token sampled at row r of the previous step.
+        ids = torch.where(ids < 0, self.last_tokens.index_select(0, (-ids - 1).clamp(min=0)), ids)
+        hidden = model.forward(ids, buffers.positions, self.engine.kv_caches, buffers.group_metadata[0])
         logits = model.logits(hidden)
-        return logits, logits.argmax(dim=-1)
+        tokens = logits.argmax(dim=-1)
+        self.last_tokens[: tokens.numel()].copy_(tokens)
+        return logits, tokens
 
     @torch.inference_mode()
     def capture(self, size: int) -> "DecodeGraph":
@@ -348,6 +435,9 @@ class DecodeGraphs:
             max_query_len=1,
         )
         self._pack(SchedulerOutput(()), buffers)  # an all-padding step: writes nothing
+        # The warm-up forwards overwrite the previous step's sampled tokens,
+        # which a pipelined step launched right after the capture still reads.
+        saved_tokens = self.last_tokens.clone()
         side = torch.cuda.Stream(e.model.device)
         side.wait_stream(torch.cuda.current_stream(e.model.device))
         with torch.cuda.stream(side):
@@ -357,6 +447,7 @@ class DecodeGraphs:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self.pool):
             logits, tokens = self.forward(buffers)
+        self.last_tokens.copy_(saved_tokens)
         entry = DecodeGraph(graph, buffers, logits, tokens)
         self.entries[size] = entry
         return entry
@@ -369,6 +460,33 @@ class DecodeGraphs:
         self._pack(plan, entry.buffers)
         entry.graph.replay()
         return entry.tokens[:n].tolist()
+
+    @torch.inference_mode()
+    def launch(self, plan: SchedulerOutput) -> "PendingStep":
+        """Replay the plan's graph and start copying its tokens to the host
+        without waiting for them (pipelined mode)."""
+
+        n = len(plan.scheduled_requests)
+        size = self.bucket(n)
+        entry = self.entries.get(size) or self.capture(size)
+        self._pack(plan, entry.buffers)
+        entry.graph.replay()
+        host = self._host[self._flip]  # alternates: the previous step's buffer is read after this launch
+        self._flip ^= 1
+        host[:n].copy_(entry.tokens[:n], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        return PendingStep(host, event)
+
+
+@dataclass
+class PendingStep:
+    """A launched graph step: its tokens arrive in `host` once `event`
+    completes; `slots` lists the (request, output index) placeholders."""
+
+    host: torch.Tensor
+    event: torch.cuda.Event
+    slots: list = field(default_factory=list)
 
 
 @dataclass

@@ -142,6 +142,32 @@ def test_fused_layer_kernels_match_reference_decoding(device, qk_norm):
     check_against_reference(requests, hip_model, ref_model, device)
 
 
+def test_pipelined_decode_matches_synchronous_decode(device):
+    """With the host one graph step ahead (placeholders for tokens still on
+    the GPU), every request's tokens equal the synchronous engine's, with
+    chunked prefill, mixed steps, a finishing request and graph buckets
+    changing size in between."""
+
+    hip_model, _ = models(device, seed=11, fused_layers=True)
+    outputs = []
+    for pipeline in (False, True):
+        requests = make_requests(seed=8, count=9, lo=10, hi=170, max_tokens=14)
+        requests[2].max_tokens = 3  # finishes early: the graph bucket shrinks
+        engine = GenerationEngine(
+            hip_model,
+            num_blocks=256,
+            max_num_batched_tokens=180,
+            max_num_seqs=6,
+            max_model_len=512,
+            decode_graphs=True,
+            pipeline=pipeline,
+        )
+        result = engine.generate(requests)
+        assert all(t >= 0 for r in requests for t in r.output_token_ids)  # no placeholder left
+        outputs.append(result.outputs)
+    assert outputs[0] == outputs[1]
+
+
 def test_decode_graph_replays_match_eager_on_the_same_buffers(device):
     """Every replay of a captured decode step equals an eager forward on the
     same static buffers, bit for bit, with eager work between replays."""
