@@ -281,7 +281,9 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed", "qwen3_e2e"])
+    parser.add_argument(
+        "--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed", "llama3_long_decode", "qwen3_e2e"]
+    )
     parser.add_argument("--e2e-requests", type=int, default=256, help="requests of the qwen3_e2e workload")
     parser.add_argument("--e2e-max-tokens", type=int, default=256, help="greedy output tokens per request (qwen3_e2e)")
     parser.add_argument("--e2e-eager", action="store_true", help="run qwen3_e2e decode steps eagerly (no HIP graphs)")
@@ -331,6 +333,12 @@ def main() -> int:
         description = (
             "qwen3_decode: 256 decode sequences, contexts U[128,4096] seed 0, 16 q / 8 kv heads, "
             "head_dim 128, block 16, bf16, 70k-block shuffled pool, values N(0,1)*0.5"
+        )
+    elif args.workload == "llama3_long_decode":
+        w = workloads.llama3_long_decode(device)
+        description = (
+            "llama3_long_decode: 64 decode sequences, contexts U[8192,33280] seed 0, 32 q / 8 kv heads, "
+            "head_dim 128, block 16, bf16, values N(0,1)"
         )
     else:
         w = workloads.llama3_mixed(device)

@@ -21,6 +21,10 @@ Named builders:
                     U[0, 2048] + 248 decodes with contexts U[256, 8192]
                     (4,344 tokens), 32 q / 8 KV heads, head_dim 128, block 16,
                     bf16, values N(0,1), shuffled pool.
+* ``llama3_long_decode``  64 decodes with contexts U[8192, 33280] (the
+                    Llama-3-8B e2e config's prefix + suffix + decode range),
+                    32 q / 8 KV heads, head_dim 128, block 16, bf16, values
+                    N(0,1), shuffled pool.
 """
 
 from __future__ import annotations
@@ -225,6 +229,36 @@ def llama3_mixed(
         "llama3_mixed",
         context_lengths=lengths,
         query_lengths=queries,
+        num_q_heads=32,
+        num_kv_heads=8,
+        head_dim=128,
+        block_size=16,
+        pool_blocks=needed + needed // 20 + 16,
+        dtype=dtype,
+        value_scale=1.0,
+        seed=seed,
+        device=device,
+        rng=rng,
+    )
+
+
+def llama3_long_decode(
+    device: torch.device | str,
+    *,
+    num_seqs: int = 64,
+    context_range: tuple[int, int] = (8192, 33280),
+    dtype: torch.dtype = torch.bfloat16,
+    seed: int = 0,
+) -> Workload:
+    """Long-context decode batch with Llama-3-8B attention heads."""
+
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(context_range[0], context_range[1] + 1, size=num_seqs)
+    needed = int(((lengths + 15) // 16).sum())
+    return build(
+        "llama3_long_decode",
+        context_lengths=lengths,
+        query_lengths=np.ones(num_seqs, dtype=np.int64),
         num_q_heads=32,
         num_kv_heads=8,
         head_dim=128,

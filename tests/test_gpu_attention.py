@@ -296,6 +296,17 @@ def test_prefill_kernel_bounded_specs(device, spec, hq, hkv):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
+def test_prefill_work_list_of_more_than_8192_slots(device):
+    """8,202 requests (8,200 of two tokens) make 8,332 work-list slots, more
+    than the sorted list holds (8,192): the list keeps slot order, and every
+    query block must still be computed exactly once."""
+
+    lengths = [300, 40] + [2] * 8200
+    qlens = [300, 17] + [2] * 8200
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 8, 8, 128, 16, seed=43)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
 def test_prefill_kernel_reloads_page_table_on_long_context(device):
     """A 40,000-key visible range spans more than one LDS page-table load
     (2,048 pages)."""
