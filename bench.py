@@ -98,6 +98,7 @@ def decode_kernel_bytes(w) -> int:
 TRAFFIC_PROFILES = {
     "qwen3_decode": ROOT / "profiles" / "decode_qwen3_256seq_traffic.md",
     "llama3_mixed": ROOT / "profiles" / "decode_llama3_mixed_traffic.md",
+    "llama3_long_decode": ROOT / "profiles" / "decode_llama3_long_kernel_stats.md",
 }
 
 

@@ -493,22 +493,38 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
     const uint32_t nan_bits = Elem<T>::to_bits(NAN);
     w[0] = w[1] = nan_bits | (nan_bits << 16);
   } else {
-    float mx = -INFINITY, sum = 0.f;
-    float4_t o = {0.f, 0.f, 0.f, 0.f};
+    // Two passes over the head's splits, 32 lanes wide: the maximum first,
+    // then every split's weight exp2(m_s - max) from its own lane, so the
+    // accumulator loads do not wait on a running maximum.
+    const int sub = threadIdx.x & 31;
     const int64_t first_item = r * a.max_splits * a.num_q_heads + hq;
-#pragma unroll 4
-    for (int64_t s = 0; s < ns; ++s) {
-      const int64_t item = first_item + s * a.num_q_heads;
-      const float2 ml = a.ws_ml[item];
-      const float4_t v = *reinterpret_cast<const float4_t*>(a.ws_acc + item * kDim + d0);
-      if (ml.x == -INFINITY) continue;
-      const float mn = fmaxf(mx, ml.x);
-      const float keep = exp2f(mx - mn);  // mx = -inf at the start: exp2(-inf) = 0
-      const float take = exp2f(ml.x - mn);
-      sum = sum * keep + take * ml.y;
-      o = o * keep + v * take;
-      mx = mn;
+    float mx = -INFINITY;
+    for (int64_t s0 = 0; s0 < ns; s0 += 32)
+      if (s0 + sub < ns) mx = fmaxf(mx, a.ws_ml[first_item + (s0 + sub) * a.num_q_heads].x);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 32));
+    float sum = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t s0 = 0; s0 < ns; s0 += 32) {
+      float w = 0.f;
+      if (s0 + sub < ns) {
+        const float2 ml = a.ws_ml[first_item + (s0 + sub) * a.num_q_heads];
+        // A split with no visible key (m = -inf) weighs 0; so does every
+        // split when none has one, and the output is then NaN (0 / 0).
+        w = ml.x == -INFINITY ? 0.f : exp2f(ml.x - mx);
+        sum += w * ml.y;
+      }
+      const int cnt = ns - s0 < 32 ? static_cast<int>(ns - s0) : 32;
+      const float* accp = a.ws_acc + (first_item + s0 * a.num_q_heads) * kDim + d0;
+#pragma unroll 8
+      for (int k = 0; k < cnt; ++k) {
+        const float wk = __shfl(w, k, 32);
+        const float4_t v = *reinterpret_cast<const float4_t*>(accp + static_cast<int64_t>(k) * a.num_q_heads * kDim);
+        o += v * wk;
+      }
     }
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 32);
     const float inv = 1.f / sum;
     w[0] = Elem<T>::to_bits(o[0] * inv) | (Elem<T>::to_bits(o[1] * inv) << 16);
     w[1] = Elem<T>::to_bits(o[2] * inv) | (Elem<T>::to_bits(o[3] * inv) << 16);
