@@ -414,6 +414,13 @@ def main() -> int:
             "kernel_bytes": int(kernel_bytes),
         },
     }
+    if args.workload == "llama3_long_decode":
+        # Host cost of caching every request's full blocks after one decode
+        # step (prefix-cache digests), the reference's from-scratch chains
+        # against incremental ones, for this batch's contexts.
+        from micro_vllm_amd.harness.prefix_hash import measure_step_cost
+
+        result["control_plane"] = {"prefix_hash": measure_step_cost(w.context_lengths.tolist(), steps=3)}
     if args.workload == "llama3_mixed":
         flops = workloads.prefill_flops(w)
         try:
