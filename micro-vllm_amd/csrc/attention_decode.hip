@@ -452,9 +452,9 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   write_decode_result<T>(a, r, qs, hq, split, decode_num_splits(lo, hi, a.split_tokens), m, lt, acc, grp);
 }
 
-// Blocks [0, R * kCombineGroups): merge split partials of multi-split
+// Blocks [0, R * head_groups): merge split partials of multi-split
 // decode requests, kCombineHeads query heads per block, 32 lanes per head
-// (4 dims each), in one pass with a running maximum.
+// (4 dims each).
 // Blocks after that: zero tokens outside every request, kZeroTokens each.
 constexpr int kZeroTokens = 16;
 constexpr int kCombineHeads = 8;
@@ -516,11 +516,20 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
       }
       const int cnt = ns - s0 < 32 ? static_cast<int>(ns - s0) : 32;
       const float* accp = a.ws_acc + (first_item + s0 * a.num_q_heads) * kDim + d0;
-#pragma unroll 8
-      for (int k = 0; k < cnt; ++k) {
-        const float wk = __shfl(w, k, 32);
-        const float4_t v = *reinterpret_cast<const float4_t*>(accp + static_cast<int64_t>(k) * a.num_q_heads * kDim);
-        o += v * wk;
+      // Eight splits per pass, their loads issued together (indices past
+      // the last split re-read it and are not added).
+      for (int k0 = 0; k0 < cnt; k0 += 8) {
+        float4_t v[8];
+        float wk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int k = k0 + j < cnt ? k0 + j : cnt - 1;
+          wk[j] = __shfl(w, k, 32);
+          v[j] = *reinterpret_cast<const float4_t*>(accp + static_cast<int64_t>(k) * a.num_q_heads * kDim);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (k0 + j < cnt) o += v[j] * wk[j];
       }
     }
 #pragma unroll

@@ -230,7 +230,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   float l = 0.f;          // this lane's share of the row's softmax sum
   const float cs = a.scale_log2;
 
-  const uint16_t* cache = static_cast<const uint16_t*>(a.cache);
   const int64_t head_elems = static_cast<int64_t>(h) * kDim;
   const int32_t base = kmax >= kmin ? (kmin & ~15) : 0;
   const int32_t ntiles = kmax >= kmin ? (kmax - base) / kTileKeys + 1 : 0;

@@ -142,6 +142,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // lane l's 16 bytes land at LDS byte address lds_base + 16 * l (lds_base is
 // wave-uniform). Issued through inline assembly so that the compiler does not
 // track the LDS write; callers order it with explicit s_waitcnt vmcnt counts.
+// The assembly sets M0, which the compiler treats as reserved (it warns about
+// the clobber): the kernels that use these loads contain no compiler-generated
+// M0 use, which their assembly shows.
 __device__ __forceinline__ void lds_dma_load16(const void* global_ptr, uint32_t lds_base) {
   asm volatile(
       "s_mov_b32 m0, %1\n\t"
