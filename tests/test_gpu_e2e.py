@@ -168,6 +168,34 @@ def test_pipelined_decode_matches_synchronous_decode(device):
     assert outputs[0] == outputs[1]
 
 
+def test_pipelined_decode_with_preemption_matches_synchronous_decode(device):
+    """A block pool too small for every request forces preemption; a victim
+    may hold a token that is still on the GPU (a placeholder) and later
+    recomputes its whole sequence. Tokens must equal the synchronous
+    engine's."""
+
+    hip_model, _ = models(device, seed=12)
+    outputs, preemptions = [], []
+    for pipeline in (False, True):
+        requests = make_requests(seed=9, count=6, lo=40, hi=90, max_tokens=40)
+        engine = GenerationEngine(
+            hip_model,
+            num_blocks=30,  # 29 usable blocks of 16 tokens for 6 requests of up to 130 tokens
+            max_num_batched_tokens=512,
+            max_num_seqs=6,
+            max_model_len=256,
+            decode_graphs=True,
+            pipeline=pipeline,
+        )
+        result = engine.generate(requests)
+        assert result.output_tokens == 6 * 40
+        assert all(t >= 0 for r in requests for t in r.output_token_ids)
+        outputs.append(result.outputs)
+        preemptions.append(result.preemptions)
+    assert preemptions[0] > 0 and preemptions[0] == preemptions[1]
+    assert outputs[0] == outputs[1]
+
+
 def test_decode_graph_replays_match_eager_on_the_same_buffers(device):
     """Every replay of a captured decode step equals an eager forward on the
     same static buffers, bit for bit, with eager work between replays."""
