@@ -31,6 +31,9 @@ struct AttnArgs {
   // request -1 marks an empty slot. Written by the item kernel before the
   // prefill kernel reads it.
   int2* items;
+  // Decode work list: (request, split) per slot, full splits first, then the
+  // partial last splits from the largest; request -1 marks an empty slot.
+  int2* decode_items;
 };
 
 // Visible key positions [lo, hi] of query `t` in request `r` whose first

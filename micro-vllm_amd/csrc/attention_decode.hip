@@ -4,6 +4,9 @@
 // owns one KV head; a workgroup holds up to 8 waves = 8 consecutive KV heads
 // of the same (request, split), so together they stream whole token rows
 // (all heads of a token are contiguous in the cache) with 16-byte loads.
+// A one-workgroup kernel lists the (request, split) items on the GPU, full
+// splits first and partial last splits from the largest down, so that the
+// grid's in-order dispatch ends on its shortest items (decode_items_kernel).
 //
 // Per 16-token tile a wave computes S^T = K . Q^T with four
 // v_mfma_f32_16x16x32 (M = 16 tokens, N = the G query heads of the KV head,
@@ -127,9 +130,13 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int waves = blockDim.x >> 6;
-  const int h = blockIdx.x * waves + wave;
-  const int split = blockIdx.y;
-  const int64_t r = blockIdx.z;
+  // 1-D grid: workgroup b takes head group b % groups of work-list slot b / groups.
+  const int groups = (a.num_kv_heads + waves - 1) / waves;
+  const int h = static_cast<int>(blockIdx.x % groups) * waves + wave;
+  const int2 item = a.decode_items[blockIdx.x / groups];
+  if (item.x < 0 || item.x >= a.num_requests) return;
+  const int split = item.y;
+  const int64_t r = item.x;
   if (h >= a.num_kv_heads) return;
   const int64_t qs = a.qsl[r];
   if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
@@ -279,9 +286,13 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int waves = blockDim.x >> 6;
-  const int h = blockIdx.x * waves + wave;
-  const int split = blockIdx.y;
-  const int64_t r = blockIdx.z;
+  // 1-D grid: workgroup b takes head group b % groups of work-list slot b / groups.
+  const int groups = (a.num_kv_heads + waves - 1) / waves;
+  const int h = static_cast<int>(blockIdx.x % groups) * waves + wave;
+  const int2 item = a.decode_items[blockIdx.x / groups];
+  if (item.x < 0 || item.x >= a.num_requests) return;
+  const int split = item.y;
+  const int64_t r = item.x;
   if (h >= a.num_kv_heads) return;
   const int64_t qs = a.qsl[r];
   if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
@@ -542,6 +553,82 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
   *reinterpret_cast<uint2*>(op + d0) = uint2{w[0], w[1]};
 }
 
+
+// ---- decode work list --------------------------------------------------------
+//
+// One workgroup lists the (request, split) items of the single-query
+// requests: every full split first (in any order), then the partial last
+// splits from the largest down, so the in-order dispatch of the decode grid
+// ends on the shortest items. Empty slots (up to R * max_splits) get
+// request -1.
+constexpr int kDecodeListThreads = 1024;
+constexpr int kSizeBuckets = 64;  // 16-token tiles of a partial split (split <= 1024)
+
+__global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnArgs a) {
+  __shared__ int32_t full_count, full_pos;
+  __shared__ int32_t bucket[kSizeBuckets];
+  const int tid = threadIdx.x;
+  const int64_t R = a.num_requests;
+  const int64_t capacity = R * a.max_splits;
+  if (tid == 0) full_count = full_pos = 0;
+  if (tid < kSizeBuckets) bucket[tid] = 0;
+  // A request's split count and last-split size (0: not a decode request).
+  auto describe = [&](int64_t r, int32_t& ns, int32_t& last) {
+    ns = 0;
+    last = 0;
+    const int64_t qs = a.qsl[r];
+    if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
+    int64_t lo, hi;
+    visible_range(a, r, qs, qs, lo, hi);
+    const int64_t n = decode_num_splits(lo, hi, a.split_tokens);
+    if (n <= 0) return;
+    ns = static_cast<int32_t>(n);
+    last = static_cast<int32_t>((hi - (lo & ~int64_t(15)) + 1) - (n - 1) * a.split_tokens);
+  };
+  // The thread's first request stays in registers between the passes.
+  int32_t ns0 = 0, last0 = 0;
+  if (tid < R) describe(tid, ns0, last0);
+  __syncthreads();
+  // Pass 1: count full splits, histogram the partial ones by size.
+  for (int64_t r = tid; r < R; r += kDecodeListThreads) {
+    int32_t ns = ns0, last = last0;
+    if (r != tid) describe(r, ns, last);
+    if (ns == 0) continue;
+    const bool partial = last < a.split_tokens;
+    atomicAdd(&full_count, partial ? ns - 1 : ns);
+    if (partial) atomicAdd(&bucket[(last - 1) >> 4], 1);
+  }
+  __syncthreads();
+  // Partial splits start after the full ones, largest bucket first: an
+  // exclusive scan over the buckets in descending order, one lane each.
+  static_assert(kSizeBuckets == 64, "one wave scans the buckets");
+  if (tid < 64) {
+    const int32_t c = bucket[63 - tid];
+    int32_t incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int32_t y = __shfl_up(incl, d, 64);
+      if (tid >= d) incl += y;
+    }
+    const int32_t fulls = full_count;
+    bucket[63 - tid] = fulls + incl - c;
+    if (tid == 63) full_count = fulls + incl;  // total number of items
+  }
+  __syncthreads();
+  // Pass 2: place the items.
+  for (int64_t r = tid; r < R; r += kDecodeListThreads) {
+    int32_t ns = ns0, last = last0;
+    if (r != tid) describe(r, ns, last);
+    if (ns == 0) continue;
+    const bool partial = last < a.split_tokens;
+    const int32_t nfull = partial ? ns - 1 : ns;
+    const int32_t at = atomicAdd(&full_pos, nfull);
+    for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = int2{static_cast<int>(r), sp};
+    if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> 4], 1)] = int2{static_cast<int>(r), ns - 1};
+  }
+  for (int64_t j = full_count + tid; j < capacity; j += kDecodeListThreads) a.decode_items[j] = int2{-1, -1};
+}
+
 struct DecodeTuning {
   bool lds_pipeline;  // the global->LDS pipelined kernel (block_size % 16 == 0)
   int waves;          // waves (KV heads) per workgroup
@@ -599,11 +686,14 @@ int launch_decode_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent
   const DecodeTuning tune = decode_tuning(a);
   const int waves = tune.waves;
   const int groups = (a.num_kv_heads + waves - 1) / waves;
-  if (a.max_splits > 65535 || a.num_requests > 65535)
-    return fail(MVLLM_ERR_INVALID, "decode grid too large (%d splits, %lld requests)",
-                a.max_splits, (long long)a.num_requests);
+
   if (a.num_requests > 0) {
-    const dim3 grid(groups, a.max_splits, static_cast<unsigned>(a.num_requests));
+    const int64_t blocks = a.num_requests * a.max_splits * groups;
+    if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "decode grid too large (%lld workgroups)", (long long)blocks);
+    if (!a.decode_items) return fail(MVLLM_ERR_INVALID, "decode work list is missing");
+    hipLaunchKernelGGL(decode_items_kernel, dim3(1), dim3(kDecodeListThreads), 0, s, a);
+    MVLLM_LAUNCH_CHECK("decode_items_kernel");
+    const dim3 grid(static_cast<unsigned>(blocks));
     const dim3 block(64 * waves);
     if (tune.lds_pipeline) {
       int rc = MVLLM_OK;

@@ -226,18 +226,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkArgs a) {
   *reinterpret_cast<uint32_t*>(dst + 2 * lane) = result;
 }
 
-// Vectorised form: one wave per token, its rows in passes of four. Lanes
-// 16 g .. 16 g + 15 hold row 4 p + g; lane j of a row holds dims 8 j .. +8
-// (16-byte loads and stores), whose rotate-half partners sit in lane j ^ 8.
-// The token's cos/sin values and cache slot are loaded once. Needs 16-byte
-// aligned rows; the kernel above covers the rest.
-template <typename T>
+// Vectorised form: a token's rows in passes of four. Lanes 16 g .. 16 g + 15
+// hold row 4 p + g; lane j of a row holds dims 8 j .. +8 (16-byte loads and
+// stores), whose rotate-half partners sit in lane j ^ 8. WHOLE_TOKEN: one
+// wave takes all of a token's passes, loading its cos/sin values and cache
+// slot once (large batches); otherwise each wave takes one pass (small
+// batches, which need the parallelism). Needs 16-byte aligned rows; the
+// kernel above covers the rest.
+template <typename T, bool WHOLE_TOKEN>
 __global__ __launch_bounds__(256) void qk_norm_rope_token_kernel(QkArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int rows = a.num_q_heads + 2 * a.num_kv_heads;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int passes = (rows + 3) / 4;
+  const int64_t t = WHOLE_TOKEN ? w : w / passes;
+  const int p_first = WHOLE_TOKEN ? 0 : static_cast<int>(w % passes) * 4;
+  const int p_end = WHOLE_TOKEN ? rows : p_first + 4;
   if (t >= a.num_tokens) return;
   const int g = lane >> 4, j = lane & 15;
-  const int rows = a.num_q_heads + 2 * a.num_kv_heads;
   float cv[8], sv[8];
   if (a.cos) {
     const float4* cp = reinterpret_cast<const float4*>(a.cos + t * 128 + 8 * j);
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token_kernel(QkArgs a) {
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   const int64_t block = slot_ok ? slot / a.block_size : 0;
   uint16_t* const kv_row = a.cache + block * a.c_s[1] + (slot_ok ? slot - block * a.block_size : 0) * a.c_s[2];
-  for (int p = 0; p < rows; p += 4) {
+  for (int p = p_first; p < p_end; p += 4) {
     const int row = p + g;
     const bool live = row < rows;
     const int rr = live ? row : rows - 1;  // idle groups repeat a valid row and store nothing
@@ -443,12 +449,19 @@ extern "C" int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query, const mvl
                    mult8(a.c_s[3]) && (!q_weight || (aligned16(q_weight) && aligned16(k_weight))) &&
                    (!cos_table || (aligned16(cos_table) && aligned16(sin_table)));
   if (vec) {
-    const int64_t blocks = (N + 3) / 4;
+    // Whole tokens per wave once the batch alone fills the GPU (>= 8 waves
+    // per CU at 256 CUs); one pass of four rows per wave below that.
+    const bool whole = N >= 2048;
+    const int64_t passes = (query->size[1] + 2 * key->size[1] + 3) / 4;
+    const int64_t blocks = ((whole ? N : N * passes) + 3) / 4;
     if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: grid too large");
-    if (dtype == MVLLM_DTYPE_BF16)
-      hipLaunchKernelGGL(qk_norm_rope_token_kernel<bf16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(qk_norm_rope_token_kernel<f16_t>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    if (dtype == MVLLM_DTYPE_BF16) {
+      if (whole) hipLaunchKernelGGL((qk_norm_rope_token_kernel<bf16_t, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((qk_norm_rope_token_kernel<bf16_t, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    } else {
+      if (whole) hipLaunchKernelGGL((qk_norm_rope_token_kernel<f16_t, true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((qk_norm_rope_token_kernel<f16_t, false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    }
     MVLLM_LAUNCH_CHECK("qk_norm_rope_token_kernel");
     return MVLLM_OK;
   }

@@ -296,6 +296,17 @@ def test_prefill_kernel_bounded_specs(device, spec, hq, hkv):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
+def test_decode_work_list_beyond_65535_slots(device):
+    """One 16,384-token context beside 4,095 short ones: 1,024-token splits,
+    17 per request, make 69,632 decode work-list slots (more than a 2-D grid
+    dimension holds); every split must be computed once and merged."""
+
+    lengths = [16_384] + [5 + (i % 60) for i in range(4095)]
+    qlens = [1] * len(lengths)
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 16, 8, 128, 16, seed=47)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
 def test_prefill_work_list_of_more_than_8192_slots(device):
     """8,202 requests (8,200 of two tokens) make 8,332 work-list slots, more
     than the sorted list holds (8,192): the list keeps slot order, and every

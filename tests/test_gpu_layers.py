@@ -137,6 +137,36 @@ def test_qk_norm_rope_kv_write_matches_torch(device, dtype, qk_norm, hq, hkv, of
     assert torch.isnan(flat[:, untouched]).all()
 
 
+def test_qk_norm_rope_kv_write_large_batch(device):
+    """2,100 tokens take the whole-token-per-wave form of the kernel."""
+
+    dtype, n, hq, hkv, d, bs = torch.bfloat16, 2100, 16, 8, 128, 16
+    nb = -(-n // bs) + 2
+    gen = torch.Generator(device=device).manual_seed(13)
+    qkv = torch.randn((n, (hq + 2 * hkv) * d), generator=gen, device=device).to(dtype)
+    q = qkv[:, : hq * d].view(n, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].view(n, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].view(n, hkv, d)
+    qw = (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(dtype)
+    kw = (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(dtype)
+    positions = torch.randint(0, 30000, (n,), generator=gen, device=device)
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32, device=device) / d))
+    angles = torch.outer(positions.float(), inv)
+    angles = torch.cat((angles, angles), dim=-1)
+    cos, sin = angles.cos().contiguous(), angles.sin().contiguous()
+    cache = torch.full((2, nb, bs, hkv, d), float("nan"), dtype=dtype, device=device)
+    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(5))[:n].to(device)
+    slots[::97] = -1
+    q_out = layers.qk_norm_rope_kv_write(q, k, v, qw, kw, cos, sin, 1e-6, cache, slots)
+    want_q, q_mag = torch_qk_rope(q, qw, cos, sin, 1e-6)
+    want_k, k_mag = torch_qk_rope(k, kw, cos, sin, 1e-6)
+    assert_rotation_close(q_out, want_q, q_mag, dtype)
+    flat = cache.view(2, -1, hkv, d)
+    keep = slots >= 0
+    assert_rotation_close(flat[0, slots[keep]], want_k[keep], k_mag[keep], dtype)
+    assert torch.equal(flat[1, slots[keep]], v[keep])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_silu_mul_matches_torch(device, dtype):
     gen = torch.Generator(device=device).manual_seed(5)
