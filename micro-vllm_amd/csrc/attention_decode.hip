@@ -589,13 +589,32 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   int32_t ns0 = 0, last0 = 0;
   if (tid < R) describe(tid, ns0, last0);
   __syncthreads();
-  // Pass 1: count full splits, histogram the partial ones by size.
-  for (int64_t r = tid; r < R; r += kDecodeListThreads) {
-    int32_t ns = ns0, last = last0;
-    if (r != tid) describe(r, ns, last);
-    if (ns == 0) continue;
-    const bool partial = last < a.split_tokens;
-    atomicAdd(&full_count, partial ? ns - 1 : ns);
+  const int lane = tid & 63;
+  // Exclusive prefix of v over the wave and the wave's total.
+  auto wave_scan = [&](int32_t v, int32_t& total) {
+    int32_t incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int32_t y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    total = __shfl(incl, 63, 64);
+    return incl - v;
+  };
+  // Pass 1: count full splits (one LDS atomic per wave), histogram the
+  // partial ones by size. The loop bound is uniform per wave.
+  for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
+    const int64_t r = r0 + lane;
+    int32_t ns = 0, last = 0;
+    if (r < R) {
+      ns = ns0;
+      last = last0;
+      if (r != tid) describe(r, ns, last);
+    }
+    const bool partial = ns > 0 && last < a.split_tokens;
+    int32_t total;
+    wave_scan(partial ? ns - 1 : ns, total);
+    if (lane == 0 && total) atomicAdd(&full_count, total);
     if (partial) atomicAdd(&bucket[(last - 1) >> 4], 1);
   }
   __syncthreads();
@@ -615,14 +634,22 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
     if (tid == 63) full_count = fulls + incl;  // total number of items
   }
   __syncthreads();
-  // Pass 2: place the items.
-  for (int64_t r = tid; r < R; r += kDecodeListThreads) {
-    int32_t ns = ns0, last = last0;
-    if (r != tid) describe(r, ns, last);
-    if (ns == 0) continue;
-    const bool partial = last < a.split_tokens;
+  // Pass 2: place the items (one LDS atomic per wave for the full splits).
+  for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
+    const int64_t r = r0 + lane;
+    int32_t ns = 0, last = 0;
+    if (r < R) {
+      ns = ns0;
+      last = last0;
+      if (r != tid) describe(r, ns, last);
+    }
+    const bool partial = ns > 0 && last < a.split_tokens;
     const int32_t nfull = partial ? ns - 1 : ns;
-    const int32_t at = atomicAdd(&full_pos, nfull);
+    int32_t total;
+    const int32_t excl = wave_scan(nfull, total);
+    int32_t at = 0;
+    if (lane == 0 && total) at = atomicAdd(&full_pos, total);
+    at = __shfl(at, 0, 64) + excl;
     for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = int2{static_cast<int>(r), sp};
     if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> 4], 1)] = int2{static_cast<int>(r), ns - 1};
   }
