@@ -12,6 +12,8 @@ Reported (one JSON line on stdout):
 * ``roofline``: the decode kernel's algorithmic bytes per launch / its mean
   duration measured with HIP events recorded around its launch, against
   the 8 TB/s HBM peak;
+* ``gpu_baseline``: the same step in plain torch (block-table gather and
+  matmuls) timed on the same GPU, and the HIP path's speedup over it;
 * ``cpu_baseline``: the numpy oracle (a restatement of the reference's
   CPU attention) timed on this host, single-threaded, on a sample of the
   same batch.
@@ -180,6 +182,110 @@ def cpu_baseline(w, sample_requests: int, repeats: int) -> dict:
     }
 
 
+def torch_gathered_attention(query, key, value, cache, md, scale: float):
+    """The operator's semantics in plain torch, as a same-box GPU baseline.
+
+    Writes K/V into the cache (``index_copy_`` on the flat slot view, padded
+    slots skipped), then per request gathers the keys of
+    [context start of its first query, context length) through the block
+    table and computes masked attention, as reference.py:14-138 does: key p
+    is visible to query t when cstart(t) <= p <= pos(t). Products run as bf16
+    (or input-dtype) ``matmul`` with the right operand made contiguous,
+    softmax in fp32. Single-query requests are batched (padded to the longest
+    context); multi-query requests run one at a time. Tokens outside every
+    request stay zero; a row with no visible key is NaN, as in the reference.
+    """
+
+    import torch
+
+    nb, bs, hkv, d = cache.shape[1:]
+    flat = cache.view(2, nb * bs, hkv, d)
+    slots = md.slot_mapping
+    keep = slots >= 0
+    idx = slots[keep]
+    flat[0].index_copy_(0, idx, key[keep])
+    flat[1].index_copy_(0, idx, value[keep])
+    n, hq, _ = query.shape
+    g = hq // hkv
+    out = torch.zeros_like(query)
+    qsl = md.query_start_locations.cpu()
+    lengths = md.context_lengths.cpu()
+    qlen = qsl[1:] - qsl[:-1]
+    table = md.block_table
+    dev = query.device
+
+    def gather(rows: torch.Tensor, pos: torch.Tensor):
+        # Slots of key positions pos[s, j] of requests rows[s]; invalid -> (0, masked).
+        blk = table[rows[:, None], (pos // bs).clamp(max=table.shape[1] - 1)]
+        ok = (blk >= 0) & (blk < nb)
+        slot = torch.where(ok, blk * bs + pos % bs, torch.zeros_like(blk))
+        return flat[0][slot], flat[1][slot], ok
+
+    single = torch.nonzero(qlen == 1).flatten()
+    if single.numel():
+        rows = single.to(dev)
+        tok = md.query_start_locations[rows]
+        lmax = int(lengths[single].max())
+        pos = torch.arange(lmax, device=dev)[None, :].expand(rows.numel(), lmax)
+        kg, vg, ok = gather(rows, pos)
+        vis = ok & (pos >= md.query_context_start_positions[tok][:, None]) & (pos <= md.query_positions[tok][:, None])
+        vis &= pos < md.context_lengths[rows][:, None]
+        q = query[tok].view(-1, hkv, g, d)
+        kt = kg.permute(0, 2, 3, 1).contiguous()  # [S, Hkv, D, L]
+        s = torch.matmul(q, kt).float() * scale    # [S, Hkv, G, L]
+        s = s.masked_fill(~vis[:, None, None, :], float("-inf"))
+        p = torch.softmax(s, dim=-1).to(query.dtype)
+        o = torch.matmul(p, vg.permute(0, 2, 1, 3).contiguous())  # [S, Hkv, G, D]
+        out[tok] = o.reshape(-1, hq, d)
+    for r in torch.nonzero(qlen > 1).flatten().tolist():
+        t0, t1, length = int(qsl[r]), int(qsl[r + 1]), int(lengths[r])
+        first = int(md.query_context_start_positions[t0])
+        pos = torch.arange(max(first, 0), length, device=dev)[None, :]
+        rows = torch.tensor([r], device=dev)
+        kg, vg, ok = gather(rows, pos)
+        cst = md.query_context_start_positions[t0:t1][:, None]
+        qp = md.query_positions[t0:t1][:, None]
+        vis = ok & (pos >= cst) & (pos <= qp)  # [n, L]
+        q = query[t0:t1].view(t1 - t0, hkv, g, d).permute(1, 2, 0, 3)  # [Hkv, G, n, D]
+        kt = kg[0].permute(1, 2, 0).contiguous()  # [Hkv, D, L]
+        s = torch.matmul(q, kt[:, None]).float() * scale  # [Hkv, G, n, L]
+        s = s.masked_fill(~vis[None, None], float("-inf"))
+        p = torch.softmax(s, dim=-1).to(query.dtype)
+        o = torch.matmul(p, vg[0].permute(1, 0, 2).contiguous()[:, None])  # [Hkv, G, n, D]
+        out[t0:t1] = o.permute(2, 0, 1, 3).reshape(t1 - t0, hq, d)
+    return out
+
+
+def torch_baseline(w, reference_out, steps: int = 5, warmup: int = 2) -> dict:
+    """Time ``torch_gathered_attention`` on the same batch and GPU."""
+
+    import math
+
+    import torch
+
+    from micro_vllm_amd import workloads
+
+    scale = 1.0 / math.sqrt(w.head_dim)
+    out = None
+    for _ in range(warmup):
+        out = torch_gathered_attention(w.query, w.key, w.value, w.cache, w.metadata, scale)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        out = torch_gathered_attention(w.query, w.key, w.value, w.cache, w.metadata, scale)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - start) * 1e3 / steps
+    diff = (out.float() - reference_out.float()).abs().nan_to_num(0.0).max().item()
+    return {
+        "value": round(workloads.decode_bytes(w) / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 4),
+        "kind": "torch gathered attention (index_copy_ write, block-table gather, bf16 matmul, fp32 softmax)",
+        "max_abs_diff_vs_hip": diff,
+        "steps": steps,
+    }
+
+
 def _subset_bytes(w, chosen) -> int:
     es = w.query.element_size()
     L = w.context_lengths[chosen]
@@ -299,6 +405,9 @@ def main() -> int:
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument(
+        "--no-torch-baseline", action="store_true", help="skip the same-box torch gathered-attention baseline"
+    )
     parser.add_argument(
         "--copy-calibration-mib",
         type=int,
@@ -442,6 +551,13 @@ def main() -> int:
         torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
+    if not args.no_torch_baseline:
+        hip_out = step(None)
+        torch.cuda.synchronize()
+        result["gpu_baseline"] = torch_baseline(w, hip_out)
+        result["gpu_baseline"]["hip_speedup"] = round(result["gpu_baseline"]["ms_per_step"] / ms_per_step, 2)
+        del hip_out
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_sample, args.cpu_repeats)
     else:

@@ -50,3 +50,59 @@ def test_more_than_one_gpu_is_refused_with_a_message():
     )
     assert result.returncode == 2
     assert "one GPU" in result.stderr
+
+
+def _oracle_case(dtype):
+    import torch
+
+    sys.path.insert(0, str(ROOT / "micro-vllm_amd"))
+    from micro_vllm_amd import workloads
+
+    from _oracle_bridge import oracle_step, to_oracle
+
+    w = workloads.small_mixed("cpu", dtype=dtype)
+    want_cache, want = oracle_step(w.query, w.key, w.value, w.cache, w.metadata)
+    got = bench.torch_gathered_attention(w.query, w.key, w.value, w.cache, w.metadata, 1.0 / np.sqrt(128))
+    return w, got, want, want_cache, to_oracle
+
+
+def test_torch_baseline_matches_the_oracle_fp32():
+    w, got, want, want_cache, to_oracle = _oracle_case(__import__("torch").float32)
+    assert np.array_equal(to_oracle(w.cache), want_cache)  # the write is bit-exact
+    np.testing.assert_allclose(got.numpy(), want, atol=2e-5, rtol=1e-5)
+
+
+def test_torch_baseline_matches_the_oracle_bf16():
+    import torch
+
+    w, got, want, want_cache, to_oracle = _oracle_case(torch.bfloat16)
+    assert np.array_equal(to_oracle(w.cache), want_cache)
+    # bf16 products (inputs rounded as the oracle's are) and bf16 output.
+    np.testing.assert_allclose(got.float().numpy(), want, atol=2e-2, rtol=1e-2)
+
+
+def test_torch_baseline_leaves_tokens_outside_requests_zero_and_empty_rows_nan():
+    import torch
+
+    sys.path.insert(0, str(ROOT / "micro-vllm_amd"))
+    from micro_vllm_amd import workloads
+
+    w = workloads.small_mixed("cpu", dtype=torch.float32)
+    md = w.metadata
+    # Drop the last request from the batch: its token is outside every request.
+    md2 = type(md)(
+        query_positions=md.query_positions,
+        query_context_start_positions=md.query_context_start_positions.clone(),
+        query_start_locations=md.query_start_locations[:-1].clone(),
+        context_lengths=md.context_lengths[:-1].clone(),
+        block_table=md.block_table[:-1].clone(),
+        slot_mapping=md.slot_mapping,
+        block_size=md.block_size,
+        max_query_len=md.max_query_len,
+    )
+    # Request 1 (a decode at position 63): its visible range starts past its position.
+    md2.query_context_start_positions[17] = 64
+    out = bench.torch_gathered_attention(w.query, w.key, w.value, w.cache, md2, 1.0 / np.sqrt(128))
+    assert torch.all(out[-1] == 0)
+    assert torch.isnan(out[17]).all()
+    assert torch.isfinite(out[18]).all()
