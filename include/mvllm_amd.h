@@ -111,8 +111,10 @@ int mvllm_kv_write(const mvllm_tensor3* key, const mvllm_tensor3* value,
 /*
  * Bytes of device workspace mvllm_paged_attention / mvllm_attention_forward
  * need for this batch geometry: the split-KV partial results of the decode
- * kernel and the prefill work list, which the library writes before it reads
- * them (the caller need not initialise the workspace). Depends only on
+ * kernel and the decode and prefill work lists, which the library writes
+ * before it reads them (the caller need not initialise the workspace).
+ * Decode positions must stay below 2^31 (block-table width * block size).
+ * Depends only on
  * shapes, never on device data, so it can be sized before graph capture.
  */
 int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch,

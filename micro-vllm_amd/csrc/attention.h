@@ -5,6 +5,15 @@
 
 namespace mvllm {
 
+// One decode work-list record: split `split` (of `ns`) of request `r`, whose
+// single query is token `qs` with visible keys [lo, hi]; the split streams
+// keys [begin, end]. Positions fit in int32 (the launcher checks the block
+// table's reach). r = -1 marks an empty slot.
+struct DecodeItem {
+  int32_t r, split, qs, ns;
+  int32_t lo, hi, begin, end;
+};
+
 // Everything a ragged paged-attention launch needs. Strides are in elements.
 struct AttnArgs {
   const void* q;
@@ -31,9 +40,10 @@ struct AttnArgs {
   // request -1 marks an empty slot. Written by the item kernel before the
   // prefill kernel reads it.
   int2* items;
-  // Decode work list: (request, split) per slot, full splits first, then the
-  // partial last splits from the largest; request -1 marks an empty slot.
-  int2* decode_items;
+  // Decode work list: one record per (request, split) slot, full splits
+  // first, then the partial last splits from the largest; r = -1 marks an
+  // empty slot.
+  DecodeItem* decode_items;
 };
 
 // Visible key positions [lo, hi] of query `t` in request `r` whose first

@@ -7,6 +7,8 @@
 // A one-workgroup kernel lists the (request, split) items on the GPU, full
 // splits first and partial last splits from the largest down, so that the
 // grid's in-order dispatch ends on its shortest items (decode_items_kernel).
+// Each record carries the request's query token, visible range and the
+// split's key range, so a workgroup needs no metadata loads of its own.
 //
 // Per 16-token tile a wave computes S^T = K . Q^T with four
 // v_mfma_f32_16x16x32 (M = 16 tokens, N = the G query heads of the KV head,
@@ -133,20 +135,16 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
   // 1-D grid: workgroup b takes head group b % groups of work-list slot b / groups.
   const int groups = (a.num_kv_heads + waves - 1) / waves;
   const int h = static_cast<int>(blockIdx.x % groups) * waves + wave;
-  const int2 item = a.decode_items[blockIdx.x / groups];
-  if (item.x < 0 || item.x >= a.num_requests) return;
-  const int split = item.y;
-  const int64_t r = item.x;
+  const DecodeItem item = a.decode_items[blockIdx.x / groups];
+  if (item.r < 0 || item.r >= a.num_requests) return;
+  const int split = item.split;
+  const int64_t r = item.r;
   if (h >= a.num_kv_heads) return;
-  const int64_t qs = a.qsl[r];
-  if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
-  int64_t lo, hi;
-  visible_range(a, r, qs, qs, lo, hi);
-  if (hi < lo) return;
-  const int64_t base0 = lo & ~int64_t(15);
-  const int64_t begin = base0 + static_cast<int64_t>(split) * a.split_tokens;
-  if (begin > hi) return;
-  const int64_t end = (begin + a.split_tokens - 1 < hi) ? begin + a.split_tokens - 1 : hi;
+  const int64_t qs = item.qs;
+  const int64_t lo = item.lo;
+  const int64_t begin = item.begin;
+  const int64_t end = item.end;
+  if (begin > end) return;
 
   // Q^T as the B operand: lane (col, grp) holds head col, dims 32i + 8grp .. +8.
   const int G = a.group;
@@ -246,7 +244,7 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
   const float l2 = l + shfl_xor_f(l, 16);
   const float lt = l2 + shfl_xor_f(l2, 32);
   if (col >= G) return;
-  write_decode_result<T>(a, r, qs, hq, split, decode_num_splits(lo, hi, a.split_tokens), m, lt, acc, grp);
+  write_decode_result<T>(a, r, qs, hq, split, item.ns, m, lt, acc, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -289,20 +287,19 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   // 1-D grid: workgroup b takes head group b % groups of work-list slot b / groups.
   const int groups = (a.num_kv_heads + waves - 1) / waves;
   const int h = static_cast<int>(blockIdx.x % groups) * waves + wave;
-  const int2 item = a.decode_items[blockIdx.x / groups];
-  if (item.x < 0 || item.x >= a.num_requests) return;
-  const int split = item.y;
-  const int64_t r = item.x;
+  // The work-list record carries the request's query token, visible range
+  // and this split's key range, so the first tile loads wait on two
+  // dependent loads (the record, then the block ids) rather than four.
+  const DecodeItem item = a.decode_items[blockIdx.x / groups];
+  if (item.r < 0 || item.r >= a.num_requests) return;
   if (h >= a.num_kv_heads) return;
-  const int64_t qs = a.qsl[r];
-  if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
-  int64_t lo, hi;
-  visible_range(a, r, qs, qs, lo, hi);
-  if (hi < lo) return;
-  const int64_t base0 = lo & ~int64_t(15);
-  const int64_t begin = base0 + static_cast<int64_t>(split) * a.split_tokens;
-  if (begin > hi) return;
-  const int64_t end = (begin + a.split_tokens - 1 < hi) ? begin + a.split_tokens - 1 : hi;
+  const int split = item.split;
+  const int64_t r = item.r;
+  const int64_t qs = item.qs;
+  const int64_t lo = item.lo;
+  const int64_t begin = item.begin;
+  const int64_t end = item.end;
+  if (begin < 0 || begin > end) return;
   const int ntiles = static_cast<int>((end - begin) / 16 + 1);  // <= 64 (split <= 1024)
 
   // Block id and in-block row of tile `lane` of this split, fetched once
@@ -460,7 +457,7 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   const float l2 = l + shfl_xor_f(l, 16);
   const float lt = l2 + shfl_xor_f(l2, 32);
   if (col >= G) return;
-  write_decode_result<T>(a, r, qs, hq, split, decode_num_splits(lo, hi, a.split_tokens), m, lt, acc, grp);
+  write_decode_result<T>(a, r, qs, hq, split, item.ns, m, lt, acc, grp);
 }
 
 // Blocks [0, R * head_groups): merge split partials of multi-split
@@ -572,22 +569,34 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   const int64_t capacity = R * a.max_splits;
   if (tid == 0) full_count = full_pos = 0;
   if (tid < kSizeBuckets) bucket[tid] = 0;
-  // A request's split count and last-split size (0: not a decode request).
-  auto describe = [&](int64_t r, int32_t& ns, int32_t& last) {
-    ns = 0;
-    last = 0;
+  // A decode request: its query token, visible keys, split count and the
+  // size of its last split (ns = 0: not a decode request).
+  struct Desc {
+    int32_t qs, lo, hi, ns, last;
+  };
+  auto describe = [&](int64_t r) {
+    Desc d = {0, 0, -1, 0, 0};
     const int64_t qs = a.qsl[r];
-    if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
+    if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return d;
     int64_t lo, hi;
     visible_range(a, r, qs, qs, lo, hi);
     const int64_t n = decode_num_splits(lo, hi, a.split_tokens);
-    if (n <= 0) return;
-    ns = static_cast<int32_t>(n);
-    last = static_cast<int32_t>((hi - (lo & ~int64_t(15)) + 1) - (n - 1) * a.split_tokens);
+    if (n <= 0) return d;
+    d.qs = static_cast<int32_t>(qs);
+    d.lo = static_cast<int32_t>(lo);
+    d.hi = static_cast<int32_t>(hi);
+    d.ns = static_cast<int32_t>(n);
+    d.last = static_cast<int32_t>((hi - (lo & ~int64_t(15)) + 1) - (n - 1) * a.split_tokens);
+    return d;
+  };
+  auto record = [&](int64_t r, const Desc& d, int32_t sp) {
+    const int32_t begin = (d.lo & ~15) + sp * a.split_tokens;
+    const int32_t end = begin + a.split_tokens - 1 < d.hi ? begin + a.split_tokens - 1 : d.hi;
+    return DecodeItem{static_cast<int32_t>(r), sp, d.qs, d.ns, d.lo, d.hi, begin, end};
   };
   // The thread's first request stays in registers between the passes.
-  int32_t ns0 = 0, last0 = 0;
-  if (tid < R) describe(tid, ns0, last0);
+  Desc d0 = {0, 0, -1, 0, 0};
+  if (tid < R) d0 = describe(tid);
   __syncthreads();
   const int lane = tid & 63;
   // Exclusive prefix of v over the wave and the wave's total.
@@ -605,12 +614,9 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   // partial ones by size. The loop bound is uniform per wave.
   for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
     const int64_t r = r0 + lane;
-    int32_t ns = 0, last = 0;
-    if (r < R) {
-      ns = ns0;
-      last = last0;
-      if (r != tid) describe(r, ns, last);
-    }
+    Desc d = {0, 0, -1, 0, 0};
+    if (r < R) d = r == tid ? d0 : describe(r);
+    const int32_t ns = d.ns, last = d.last;
     const bool partial = ns > 0 && last < a.split_tokens;
     int32_t total;
     wave_scan(partial ? ns - 1 : ns, total);
@@ -637,12 +643,9 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   // Pass 2: place the items (one LDS atomic per wave for the full splits).
   for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
     const int64_t r = r0 + lane;
-    int32_t ns = 0, last = 0;
-    if (r < R) {
-      ns = ns0;
-      last = last0;
-      if (r != tid) describe(r, ns, last);
-    }
+    Desc d = {0, 0, -1, 0, 0};
+    if (r < R) d = r == tid ? d0 : describe(r);
+    const int32_t ns = d.ns, last = d.last;
     const bool partial = ns > 0 && last < a.split_tokens;
     const int32_t nfull = partial ? ns - 1 : ns;
     int32_t total;
@@ -650,10 +653,11 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
     int32_t at = 0;
     if (lane == 0 && total) at = atomicAdd(&full_pos, total);
     at = __shfl(at, 0, 64) + excl;
-    for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = int2{static_cast<int>(r), sp};
-    if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> 4], 1)] = int2{static_cast<int>(r), ns - 1};
+    for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = record(r, d, sp);
+    if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> 4], 1)] = record(r, d, ns - 1);
   }
-  for (int64_t j = full_count + tid; j < capacity; j += kDecodeListThreads) a.decode_items[j] = int2{-1, -1};
+  for (int64_t j = full_count + tid; j < capacity; j += kDecodeListThreads)
+    a.decode_items[j] = DecodeItem{-1, -1, 0, 0, 0, -1, 0, -1};
 }
 
 struct DecodeTuning {
@@ -718,6 +722,9 @@ int launch_decode_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent
     const int64_t blocks = a.num_requests * a.max_splits * groups;
     if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "decode grid too large (%lld workgroups)", (long long)blocks);
     if (!a.decode_items) return fail(MVLLM_ERR_INVALID, "decode work list is missing");
+    // Work-list records carry positions and token indices as int32.
+    if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX)
+      return fail(MVLLM_ERR_UNSUPPORTED, "decode positions beyond 2^31 are not supported");
     hipLaunchKernelGGL(decode_items_kernel, dim3(1), dim3(kDecodeListThreads), 0, s, a);
     MVLLM_LAUNCH_CHECK("decode_items_kernel");
     const dim3 grid(static_cast<unsigned>(blocks));
