@@ -14,6 +14,16 @@ struct DecodeItem {
   int32_t lo, hi, begin, end;
 };
 
+// One prefill work-list record: query tokens [t0, t1) of request `r` (whose
+// first query is token `qs`); lo is the first visible key of row t0 and hi
+// the last visible key of row t1 - 1 (their hull covers every row when
+// visible ranges grow with the token, which the kernel checks). r = -1
+// marks an empty slot.
+struct PrefillItem {
+  int32_t r, t0, t1, qs;
+  int32_t lo, hi, pad0, pad1;
+};
+
 // Everything a ragged paged-attention launch needs. Strides are in elements.
 struct AttnArgs {
   const void* q;
@@ -36,10 +46,10 @@ struct AttnArgs {
   float2* ws_ml;
   int32_t split_tokens, max_splits;
   int32_t mode;  // generic kernel: 0 = every token; 1 = only requests with > 1 query
-  // Prefill work list: (request, query block) per slot, heaviest first;
-  // request -1 marks an empty slot. Written by the item kernel before the
+  // Prefill work list: one record per (request, query block) slot, heaviest
+  // first; r = -1 marks an empty slot. Written by the item kernel before the
   // prefill kernel reads it.
-  int2* items;
+  PrefillItem* items;
   // Decode work list: one record per (request, split) slot, full splits
   // first, then the partial last splits from the largest; r = -1 marks an
   // empty slot.

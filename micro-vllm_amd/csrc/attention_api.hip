@@ -53,7 +53,7 @@ struct DecodeLayout {
   int32_t max_splits;
   int64_t acc_bytes;
   int64_t ml_bytes;
-  int64_t items_bytes;  // prefill work list: one int2 per slot, N / 8 + R slots at most
+  int64_t items_bytes;  // prefill work list: one 32-byte record per slot, N / 8 + R slots at most
   int64_t decode_items_bytes;  // decode work list: one 32-byte record per (request, split)
   int64_t total() const { return acc_bytes + ml_bytes + items_bytes + decode_items_bytes; }
 };
@@ -69,7 +69,7 @@ DecodeLayout decode_layout(const mvllm_batch* b, int64_t num_q_heads, int64_t he
   d.acc_bytes = (items * head_dim * 4 + 255) / 256 * 256;
   d.ml_bytes = (items * 8 + 255) / 256 * 256;
   // Prefill query blocks hold T = 128 / G >= 8 tokens.
-  d.items_bytes = ((b->num_tokens / 8 + b->num_requests) * 8 + 255) / 256 * 256;
+  d.items_bytes = ((b->num_tokens / 8 + b->num_requests) * static_cast<int64_t>(sizeof(PrefillItem)) + 255) / 256 * 256;
   d.decode_items_bytes = (b->num_requests * d.max_splits * static_cast<int64_t>(sizeof(DecodeItem)) + 255) / 256 * 256;
   return d;
 }
@@ -190,7 +190,7 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
   a.max_splits = d.max_splits;
   a.ws_acc = static_cast<float*>(workspace);
   a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + d.acc_bytes);
-  a.items = reinterpret_cast<int2*>(static_cast<char*>(workspace) + d.acc_bytes + d.ml_bytes);
+  a.items = reinterpret_cast<PrefillItem*>(static_cast<char*>(workspace) + d.acc_bytes + d.ml_bytes);
   a.decode_items = reinterpret_cast<DecodeItem*>(static_cast<char*>(workspace) + d.acc_bytes + d.ml_bytes + d.items_bytes);
   hipEvent_t ds = timing ? static_cast<hipEvent_t>(timing->decode_start) : nullptr;
   hipEvent_t de = timing ? static_cast<hipEvent_t>(timing->decode_stop) : nullptr;

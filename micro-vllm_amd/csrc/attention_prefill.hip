@@ -167,15 +167,20 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   const int h = static_cast<int>(blockIdx.x % Hkv);
   const int64_t slot = static_cast<int64_t>(blockIdx.x / Hkv);
   if (slot >= nblk) return;
-  const int2 item = a.items[slot];
-  if (item.x < 0 || item.x >= R) return;
-  const int64_t r = item.x;
-  const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
-  if (qs < 0 || qe > a.num_tokens || qe - qs <= 1) return;
-  const int64_t b = item.y;
-  const int64_t t0 = qs + b * tpb;
-  if (b < 0 || t0 >= qe) return;
-  const int64_t t1 = t0 + tpb < qe ? t0 + tpb : qe;
+  // The record carries the rows' tokens and the hull [first row's first
+  // key, last row's last key], so the page table of that range is fetched
+  // while the rows' own ranges load; one barrier then publishes both.
+  const PrefillItem item = a.items[slot];
+  if (item.r < 0 || item.r >= R) return;
+  const int64_t r = item.r;
+  const int64_t qs = item.qs;
+  const int64_t t0 = item.t0;
+  const int64_t t1 = item.t1;
+  if (qs < 0 || t0 < qs || t0 >= t1 || t1 > a.num_tokens) return;
+  const int32_t hull_lo = item.lo, hull_hi = item.hi;
+  const bool hull_ok = hull_hi >= hull_lo;
+  const int32_t hull_base = hull_ok ? (hull_lo & ~15) : 0;
+  const int32_t hull_tiles = hull_ok ? (hull_hi - hull_base) / kTileKeys + 1 : 0;
 
   // ---- rows of this lane: (head hg of the group, token tok)
   const int f = wave * 32 + n;
@@ -193,6 +198,15 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     }
   }
   const bool nonempty = hi_n >= lo_n;
+  // Block ids of the hull's first chunk of pages (pages past its last key
+  // are never looked up: their table entries may be anything).
+  {
+    const int32_t nt = hull_tiles < kChunkTiles ? hull_tiles : kChunkTiles;
+    for (int i = tid; i < nt * 4; i += 256) {
+      const int32_t pos = hull_base + 16 * i;
+      page_tbl[i] = pos <= hull_hi ? static_cast<int32_t>(block_of(a, r, pos)) : -1;
+    }
+  }
   // Wave-uniform bounds of the wave's rows' visible ranges.
   const int32_t w_lo_min = __builtin_amdgcn_readfirstlane(wave_min_i(nonempty ? lo_n : INT_MAX));
   const int32_t w_lo_max = __builtin_amdgcn_readfirstlane(wave_max_i(nonempty ? lo_n : INT_MIN));
@@ -222,6 +236,14 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   }
   kmin = __builtin_amdgcn_readfirstlane(kmin);
   kmax = __builtin_amdgcn_readfirstlane(kmax);
+  // Rows inside the hull (always, when ranges grow with the token): keys
+  // [hull_lo, hull_hi], whose first chunk of block ids is already in LDS.
+  // Otherwise the rows' own bounds, and the table is fetched again.
+  const bool hull_table = kmax >= kmin && kmin >= hull_lo && kmax <= hull_hi;
+  if (hull_table) {
+    kmin = hull_lo;
+    kmax = hull_hi;
+  }
 
   float16v oacc[4];
 #pragma unroll
@@ -273,11 +295,13 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     const int32_t nt = ntiles - c0 < kChunkTiles ? ntiles - c0 : kChunkTiles;
     // Block ids of the chunk's pages; pages past the last visible key are
     // never looked up (their table entries may be anything).
-    for (int i = tid; i < nt * 4; i += 256) {
-      const int32_t pos = base + kTileKeys * c0 + 16 * i;
-      page_tbl[i] = pos <= kmax ? static_cast<int32_t>(block_of(a, r, pos)) : -1;
+    if (c0 > 0 || !hull_table) {
+      for (int i = tid; i < nt * 4; i += 256) {
+        const int32_t pos = base + kTileKeys * c0 + 16 * i;
+        page_tbl[i] = pos <= kmax ? static_cast<int32_t>(block_of(a, r, pos)) : -1;
+      }
+      __syncthreads();
     }
-    __syncthreads();
 
     // Wave w moves page w of each tile into LDS (K and V), four 1 KiB
     // instructions each. Byte address of the K page segment of tile tl:
@@ -491,17 +515,34 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   }
 
   const float lt = sum_with_partner(l);
-  if (!row_ok) return;
   // O^T block c, register 4 q + e of lane (n, hh): dim 32 c + 8 q + 4 hh + e.
+  // Lanes n and n + 32 hold the two halves of each 8-dim group 8 q; one
+  // v_permlane32_swap per word gives lane hh the whole group q = 2 p + hh,
+  // so every lane writes 16-byte pieces.
   const float inv = nonempty ? 1.f / lt : NAN;  // an empty visible range is NaN, as in the reference
-  uint16_t* op = static_cast<uint16_t*>(a.out) + tok * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1 + 4 * hh;
+  uint16_t* op = static_cast<uint16_t*>(a.out) + tok * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1;
 #pragma unroll
   for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t w0 = Mma32<T>::pack2(oacc[c][4 * q] * inv, oacc[c][4 * q + 1] * inv);
-      const uint32_t w1 = Mma32<T>::pack2(oacc[c][4 * q + 2] * inv, oacc[c][4 * q + 3] * inv);
-      *reinterpret_cast<uint2*>(op + 32 * c + 8 * q) = uint2{w0, w1};
+    for (int p = 0; p < 2; ++p) {
+      uint32_t w[2][2];  // [q - 2 p][word]
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int q = 2 * p + u;
+        w[u][0] = Mma32<T>::pack2(oacc[c][4 * q] * inv, oacc[c][4 * q + 1] * inv);
+        w[u][1] = Mma32<T>::pack2(oacc[c][4 * q + 2] * inv, oacc[c][4 * q + 3] * inv);
+      }
+      // Lane hh keeps its half of group 2 p + hh and sends its half of the
+      // other group to its partner.
+      uint32_t got[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint32_t send = hh ? w[0][k] : w[1][k];
+        const auto r2 = __builtin_amdgcn_permlane32_swap(send, send, false, false);
+        got[k] = hh ? r2[0] : r2[1];
+      }
+      const uint4 piece = hh ? uint4{got[0], got[1], w[1][0], w[1][1]} : uint4{w[0][0], w[0][1], got[0], got[1]};
+      if (row_ok) *reinterpret_cast<uint4*>(op + 32 * c + 8 * (2 * p + hh)) = piece;
     }
 }
 
@@ -530,6 +571,18 @@ __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a,
   const int64_t tpb = int64_t{1} << lg_tok;
   const int64_t R = a.num_requests;
   const int64_t nslots = a.num_tokens / tpb + R;
+  // Record of query block b of request r (its first query is qs, its last
+  // query token qe - 1).
+  auto record = [&](int64_t r, int64_t qs, int64_t qe, int64_t b) {
+    const int64_t t0 = qs + b * tpb;
+    const int64_t t1 = t0 + tpb < qe ? t0 + tpb : qe;
+    int64_t lo0, hi0, lo1, hi1;
+    visible_range(a, r, qs, t0, lo0, hi0);
+    visible_range(a, r, qs, t1 - 1, lo1, hi1);
+    return PrefillItem{static_cast<int32_t>(r), static_cast<int32_t>(t0), static_cast<int32_t>(t1),
+                       static_cast<int32_t>(qs), static_cast<int32_t>(lo0), static_cast<int32_t>(hi1), 0, 0};
+  };
+  const PrefillItem empty = {-1, 0, 0, 0, 0, -1, 0, 0};
   if (nslots > kItemSlots) {
     for (int64_t j = tid; j < nslots; j += kItemThreads) {
       int64_t rl = 0, rh = R - 1;
@@ -540,7 +593,7 @@ __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a,
       const int64_t qs = a.qsl[rl], qe = a.qsl[rl + 1];
       const int64_t b = j - (qs / tpb + rl);
       const bool ok = qs >= 0 && qe <= a.num_tokens && qe - qs > 1 && b >= 0 && qs + b * tpb < qe;
-      a.items[nslots - 1 - j] = ok ? int2{static_cast<int>(rl), static_cast<int>(b)} : int2{-1, -1};
+      a.items[nslots - 1 - j] = ok ? record(rl, qs, qe, b) : empty;
     }
     return;
   }
@@ -600,9 +653,10 @@ __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a,
     const int32_t r = owner[j];
     if (r < 0) continue;
     const int pos = atomicAdd(&start[bucket_of[j]], 1);
-    a.items[pos] = int2{r, static_cast<int>(j - (a.qsl[r] / tpb + r))};
+    const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
+    a.items[pos] = record(r, qs, qe, j - (qs / tpb + r));
   }
-  for (int64_t j = total + tid; j < nslots; j += kItemThreads) a.items[j] = int2{-1, -1};
+  for (int64_t j = total + tid; j < nslots; j += kItemThreads) a.items[j] = empty;
 }
 
 template <typename T, bool PSPLIT>
