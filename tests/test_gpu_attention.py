@@ -318,6 +318,28 @@ def test_prefill_work_list_of_more_than_8192_slots(device):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
+@pytest.mark.parametrize(("hq", "hkv"), [(16, 8), (32, 8)], ids=["qwen3", "llama3"])
+def test_prefill_kernel_rows_outside_the_work_list_hull(device, hq, hkv):
+    """Context starts that do not grow with the token: every fifth query sees
+    from key 0, the others only their last 64 keys. Rows of a query block
+    then reach keys before the block's first row's start (the work-list
+    record's hull), and the kernel must fall back to the rows' own bounds."""
+
+    q, k, v, cache, md = build_case(device, torch.bfloat16, [600, 300], [400, 300], hq, hkv, 128, 16, seed=53)
+    pos = md.query_positions
+    starts = torch.where(pos % 5 == 0, torch.zeros_like(pos), (pos - 64).clamp(min=0))
+    md = AttentionMetadata(
+        query_positions=md.query_positions,
+        query_context_start_positions=starts,
+        query_start_locations=md.query_start_locations,
+        context_lengths=md.context_lengths,
+        block_table=md.block_table,
+        slot_mapping=md.slot_mapping,
+        block_size=md.block_size,
+    )
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
 def test_prefill_kernel_reloads_page_table_on_long_context(device):
     """A 40,000-key visible range spans more than one LDS page-table load
     (2,048 pages)."""
