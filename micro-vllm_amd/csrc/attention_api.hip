@@ -43,11 +43,11 @@ int32_t decode_split_tokens(int64_t num_requests, int64_t max_context) {
   int64_t split = (est_tokens + target_items - 1) / target_items;
   split = (split + 15) / 16 * 16;
   if (split < 64) split = 64;
-  // The pipelined decode kernel reads a split's block ids once, one 16-token
-  // tile per lane, so it takes splits of up to 1024 tokens; longer splits
+  // The pipelined decode kernel reads a split's block ids once, two 16-token
+  // tiles per lane, so it takes splits of up to 2048 tokens; longer splits
   // would fall back to the general kernel, which streams ~15% slower
   // (64 contexts of 8k-33k tokens: 916 vs 1097 us).
-  if (split > 1024) split = 1024;
+  if (split > 2048) split = 2048;
   return static_cast<int32_t>(split);
 }
 

@@ -300,16 +300,27 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   const int64_t begin = item.begin;
   const int64_t end = item.end;
   if (begin < 0 || begin > end) return;
-  const int ntiles = static_cast<int>((end - begin) / 16 + 1);  // <= 64 (split <= 1024)
+  const int ntiles = static_cast<int>((end - begin) / 16 + 1);  // <= 128 (split <= 2048)
 
-  // Block id and in-block row of tile `lane` of this split, fetched once
-  // (block ids are < 2^31; a 16-aligned tile never straddles a block).
-  int32_t my_block = -1, my_row = 0;
-  if (lane < ntiles) {
-    const int64_t p = begin + 16 * lane;
-    my_block = static_cast<int32_t>(block_of(a, r, p));
-    my_row = static_cast<int32_t>(p % a.block_size);
+  // Block id and in-block row of tiles `lane` and `lane + 64` of this split,
+  // fetched once (block ids are < 2^31; a 16-aligned tile never straddles a
+  // block).
+  int32_t my_block[2] = {-1, -1}, my_row[2] = {0, 0};
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    if (lane + 64 * x < ntiles) {
+      const int64_t p = begin + 16 * (lane + 64 * x);
+      my_block[x] = static_cast<int32_t>(block_of(a, r, p));
+      my_row[x] = static_cast<int32_t>(p % a.block_size);
+    }
   }
+  // Tile t's block id and row (t wave-uniform).
+  auto tile_block = [&](int t) {
+    return t < 64 ? __builtin_amdgcn_readlane(my_block[0], t) : __builtin_amdgcn_readlane(my_block[1], t - 64);
+  };
+  auto tile_row = [&](int t) {
+    return t < 64 ? __builtin_amdgcn_readlane(my_row[0], t) : __builtin_amdgcn_readlane(my_row[1], t - 64);
+  };
 
   const int G = a.group;
   const int hq = h * G + col;
@@ -338,8 +349,8 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   }
 
   auto issue = [&](int tile, int stage) {
-    const int32_t blk = __builtin_amdgcn_readlane(my_block, tile);
-    const int32_t row = __builtin_amdgcn_readlane(my_row, tile);
+    const int32_t blk = tile_block(tile);
+    const int32_t row = tile_row(tile);
     const uint32_t kdst = wave_lds_addr + stage * 2 * kTileBytes;
     const uint32_t vdst = kdst + kTileBytes;
     // An invalid block id masks the whole tile: read a valid dummy line instead.
@@ -382,7 +393,7 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
     compiler_fence();
 
     const int64_t tb = begin + 16 * static_cast<int64_t>(k);
-    const int64_t blk = __builtin_amdgcn_readlane(my_block, k);
+    const int64_t blk = tile_block(k);
     // Token j of the tile is visible iff its position is in [lo, end] and the block is valid.
     uint32_t okmask = 0;
     if (blk >= 0) {
@@ -559,7 +570,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
 // ends on the shortest items. Empty slots (up to R * max_splits) get
 // request -1.
 constexpr int kDecodeListThreads = 1024;
-constexpr int kSizeBuckets = 64;  // 16-token tiles of a partial split (split <= 1024)
+constexpr int kSizeBuckets = 64;  // sizes of a partial split, 16 or 32 tokens each (split <= 2048)
 
 __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnArgs a) {
   __shared__ int32_t full_count, full_pos;
@@ -567,6 +578,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   const int tid = threadIdx.x;
   const int64_t R = a.num_requests;
   const int64_t capacity = R * a.max_splits;
+  const int bucket_shift = a.split_tokens > 1024 ? 5 : 4;  // 64 buckets span the split
   if (tid == 0) full_count = full_pos = 0;
   if (tid < kSizeBuckets) bucket[tid] = 0;
   // A decode request: its query token, visible keys, split count and the
@@ -621,7 +633,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
     int32_t total;
     wave_scan(partial ? ns - 1 : ns, total);
     if (lane == 0 && total) atomicAdd(&full_count, total);
-    if (partial) atomicAdd(&bucket[(last - 1) >> 4], 1);
+    if (partial) atomicAdd(&bucket[(last - 1) >> bucket_shift], 1);
   }
   __syncthreads();
   // Partial splits start after the full ones, largest bucket first: an
@@ -654,7 +666,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
     if (lane == 0 && total) at = atomicAdd(&full_pos, total);
     at = __shfl(at, 0, 64) + excl;
     for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = record(r, d, sp);
-    if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> 4], 1)] = record(r, d, ns - 1);
+    if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> bucket_shift], 1)] = record(r, d, ns - 1);
   }
   for (int64_t j = full_count + tid; j < capacity; j += kDecodeListThreads)
     a.decode_items[j] = DecodeItem{-1, -1, 0, 0, 0, -1, 0, -1};
@@ -670,7 +682,7 @@ struct DecodeTuning {
 
 DecodeTuning decode_tuning(const AttnArgs& a) {
   DecodeTuning t;
-  t.lds_pipeline = a.block_size % 16 == 0 && a.split_tokens <= 1024;
+  t.lds_pipeline = a.block_size % 16 == 0 && a.split_tokens <= 2048;
   t.waves = 4;
   t.stages = 2;
   t.prefetch = false;

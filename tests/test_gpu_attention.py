@@ -296,11 +296,12 @@ def test_prefill_kernel_bounded_specs(device, spec, hq, hkv):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
-def test_decode_work_list_beyond_65535_slots(device):
+def test_decode_work_list_beyond_65535_slots(device, monkeypatch):
     """One 16,384-token context beside 4,095 short ones: 1,024-token splits,
     17 per request, make 69,632 decode work-list slots (more than a 2-D grid
     dimension holds); every split must be computed once and merged."""
 
+    monkeypatch.setenv("MVLLM_DECODE_SPLIT", "1024")
     lengths = [16_384] + [5 + (i % 60) for i in range(4095)]
     qlens = [1] * len(lengths)
     q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 16, 8, 128, 16, seed=47)
@@ -475,6 +476,8 @@ DECODE_VARIANTS = [
     {"MVLLM_DECODE_STAGES": "4", "MVLLM_DECODE_WAVES": "1"},
     {"MVLLM_DECODE_SPLIT": "64"},
     {"MVLLM_DECODE_SPLIT": "1024"},
+    {"MVLLM_DECODE_SPLIT": "1536"},
+    {"MVLLM_DECODE_SPLIT": "2048"},
 ]
 
 
