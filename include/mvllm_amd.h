@@ -137,6 +137,36 @@ int mvllm_paged_attention(const mvllm_tensor3* query,
                           int64_t workspace_bytes, void* stream);
 
 /*
+ * Writes the work lists of `batch` (the decode split list, the per-request
+ * decode table and the prefill query-block list) into `workspace`, for
+ * mvllm_paged_attention_planned. The workspace is sized by
+ * mvllm_attention_workspace_bytes(batch, num_q_heads, head_dim) for the
+ * cache's head_dim. No counterpart in the reference, whose operator runs per
+ * layer (qwen.py:89-99): its callers are models whose layers share one batch
+ * and one cache geometry, which then plan once per step instead of once per
+ * layer (the lists depend only on the batch). Graph-capturable.
+ */
+int mvllm_attention_plan(const mvllm_batch* batch, int64_t num_q_heads,
+                         const mvllm_kv_cache* cache, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/*
+ * mvllm_paged_attention over the work lists that mvllm_attention_plan wrote
+ * into the same workspace. The caller guarantees that the plan was made for
+ * this batch, head count and cache geometry, and that nothing overwrote the
+ * workspace since (calls in one stream may share it: each rewrites only the
+ * split-KV partials). This is not checked; a mismatched plan gives wrong
+ * results but every record field is range-checked before it is used as an
+ * index.
+ */
+int mvllm_paged_attention_planned(const mvllm_tensor3* query,
+                                  const mvllm_kv_cache* cache,
+                                  const mvllm_batch* batch,
+                                  const mvllm_tensor3* out, float scale,
+                                  void* workspace, int64_t workspace_bytes,
+                                  void* stream);
+
+/*
  * The whole operator: mvllm_kv_write(key, value, slot_mapping) followed by
  * mvllm_paged_attention. Replaces AttentionOperator.forward
  * (base.py:30-40) as implemented by ReferenceAttentionOperator.forward
@@ -307,7 +337,7 @@ const char* mvllm_last_error(void);
 /* ABI version of this header (bumped on incompatible change). */
 int mvllm_abi_version(void);
 
-#define MVLLM_ABI_VERSION 3
+#define MVLLM_ABI_VERSION 4
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,14 @@ struct AttnArgs {
   // first, then the partial last splits from the largest; r = -1 marks an
   // empty slot.
   DecodeItem* decode_items;
+  // Per request, written with the decode work list: (query token, number of
+  // splits), or (0, -1) for a request that is not a single-query decode. The
+  // combine kernel reads it instead of re-deriving the visible range.
+  int2* decode_req;
+  // Host side only: the work lists and the per-request table are already in
+  // the workspace (planned once for a step), so the launches skip the
+  // work-list kernels.
+  int32_t lists_ready;
 };
 
 // Visible key positions [lo, hi] of query `t` in request `r` whose first
@@ -92,6 +100,9 @@ __device__ __forceinline__ int64_t decode_num_splits(int64_t lo, int64_t hi, int
 int launch_generic(const AttnArgs& a, int32_t dtype, hipStream_t s);
 int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t start,
                   hipEvent_t stop);
+// The work-list kernels alone (decode list + per-request table; prefill list).
+int launch_decode_lists(const AttnArgs& a, hipStream_t s);
+int launch_prefill_lists(const AttnArgs& a, hipStream_t s);
 int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t start,
                    hipEvent_t stop);
 bool prefill_supported(const AttnArgs& a, int32_t dtype);

@@ -58,7 +58,8 @@ struct DecodeLayout {
   int64_t ml_bytes;
   int64_t items_bytes;  // prefill work list: one 32-byte record per slot, N / 8 + R slots at most
   int64_t decode_items_bytes;  // decode work list: one 32-byte record per (request, split)
-  int64_t total() const { return acc_bytes + ml_bytes + items_bytes + decode_items_bytes; }
+  int64_t decode_req_bytes;  // per request (query token, splits) for the combine kernel
+  int64_t total() const { return acc_bytes + ml_bytes + items_bytes + decode_items_bytes + decode_req_bytes; }
 };
 
 DecodeLayout decode_layout(const mvllm_batch* b, int64_t num_q_heads, int64_t head_dim) {
@@ -74,6 +75,7 @@ DecodeLayout decode_layout(const mvllm_batch* b, int64_t num_q_heads, int64_t he
   // Prefill query blocks hold T = 128 / G >= 8 tokens.
   d.items_bytes = ((b->num_tokens / 8 + b->num_requests) * static_cast<int64_t>(sizeof(PrefillItem)) + 255) / 256 * 256;
   d.decode_items_bytes = (b->num_requests * d.max_splits * static_cast<int64_t>(sizeof(DecodeItem)) + 255) / 256 * 256;
+  d.decode_req_bytes = (b->num_requests * 8 + 255) / 256 * 256;
   return d;
 }
 
@@ -121,10 +123,79 @@ extern "C" int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch, int
 namespace mvllm {
 namespace {
 
+// Batch and cache fields of the kernel arguments.
+void fill_batch_args(AttnArgs& a, const mvllm_batch* batch, const mvllm_kv_cache* cache, int64_t Hq) {
+  a.cache = cache->data;
+  for (int i = 0; i < 5; ++i) a.c_s[i] = cache->stride[i];
+  a.positions = batch->query_positions;
+  a.cstarts = batch->query_context_start_positions;
+  a.qsl = batch->query_start_locations;
+  a.lengths = batch->context_lengths;
+  a.table = batch->block_table;
+  a.t_s0 = batch->block_table_stride[0];
+  a.t_s1 = batch->block_table_stride[1];
+  a.width = batch->block_table_width;
+  a.num_tokens = batch->num_tokens;
+  a.num_requests = batch->num_requests;
+  a.num_blocks = cache->num_blocks;
+  a.block_size = cache->block_size;
+  a.num_q_heads = static_cast<int32_t>(Hq);
+  a.num_kv_heads = static_cast<int32_t>(cache->num_kv_heads);
+  a.group = static_cast<int32_t>(Hq / cache->num_kv_heads);
+  a.head_dim = static_cast<int32_t>(cache->head_dim);
+}
+
+// The cache-side conditions of the MFMA kernels (the query and output add
+// their own): a plan is built whenever a planned call can take that path.
+bool fast_cache(const mvllm_kv_cache* cache, int64_t group) {
+  const int32_t dtype = cache->dtype;
+  const int64_t es = dtype_bytes(dtype);
+  return (dtype == MVLLM_DTYPE_BF16 || dtype == MVLLM_DTYPE_F16) && cache->head_dim == 128 && group <= 16 &&
+         cache->stride[4] == 1 && cache->stride[3] == cache->head_dim && vec16(cache->stride[0], es) &&
+         vec16(cache->stride[1], es) && vec16(cache->stride[2], es) && aligned16(cache->data);
+}
+
+// Split-KV partials, work lists and the per-request table in the workspace.
+int bind_workspace(AttnArgs& a, const mvllm_batch* batch, int64_t Hq, int64_t D, void* workspace,
+                   int64_t workspace_bytes) {
+  const DecodeLayout d = decode_layout(batch, Hq, D);
+  if (workspace_bytes < d.total() || (!workspace && d.total() > 0))
+    return fail(MVLLM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld required",
+                (long long)workspace_bytes, (long long)d.total());
+  if (!aligned16(workspace)) return fail(MVLLM_ERR_INVALID, "workspace must be 16-byte aligned");
+  char* const w = static_cast<char*>(workspace);
+  a.split_tokens = d.split_tokens;
+  a.max_splits = d.max_splits;
+  a.ws_acc = reinterpret_cast<float*>(w);
+  a.ws_ml = reinterpret_cast<float2*>(w + d.acc_bytes);
+  a.items = reinterpret_cast<PrefillItem*>(w + d.acc_bytes + d.ml_bytes);
+  a.decode_items = reinterpret_cast<DecodeItem*>(w + d.acc_bytes + d.ml_bytes + d.items_bytes);
+  a.decode_req = reinterpret_cast<int2*>(w + d.acc_bytes + d.ml_bytes + d.items_bytes + d.decode_items_bytes);
+  return MVLLM_OK;
+}
+
+int attention_plan(const mvllm_batch* batch, int64_t Hq, const mvllm_kv_cache* cache, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  if (!cache || !cache->data) return fail(MVLLM_ERR_INVALID, "cache is null");
+  if (int rc = check_batch(batch, cache)) return rc;
+  const int64_t Hkv = cache->num_kv_heads, D = cache->head_dim;
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
+    return fail(MVLLM_ERR_INVALID, "query heads %lld not a multiple of KV heads %lld", (long long)Hq,
+                (long long)Hkv);
+  if (batch->num_tokens == 0 || batch->num_requests == 0 || !fast_cache(cache, Hq / Hkv)) return MVLLM_OK;
+  AttnArgs a = {};
+  fill_batch_args(a, batch, cache, Hq);
+  if (int rc = bind_workspace(a, batch, Hq, D, workspace, workspace_bytes)) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = launch_decode_lists(a, s)) return rc;
+  if (batch->max_query_len == 1 || !prefill_supported(a, cache->dtype)) return MVLLM_OK;
+  return launch_prefill_lists(a, s);
+}
+
 int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
                     const mvllm_batch* batch, const mvllm_tensor3* out, float scale,
                     void* workspace, int64_t workspace_bytes, const mvllm_timing* timing,
-                    void* stream) {
+                    void* stream, bool planned = false) {
   if (int rc = check_tensor(query, "query")) return rc;
   if (int rc = check_tensor(out, "out")) return rc;
   if (!cache || !cache->data) return fail(MVLLM_ERR_INVALID, "cache is null");
@@ -147,54 +218,24 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
   if (Hq > 65535 || D > 65535) return fail(MVLLM_ERR_INVALID, "head count or head_dim too large");
 
   AttnArgs a = {};
+  fill_batch_args(a, batch, cache, Hq);
   a.q = query->data;
   a.q_s0 = query->stride[0]; a.q_s1 = query->stride[1]; a.q_s2 = query->stride[2];
-  a.cache = cache->data;
-  for (int i = 0; i < 5; ++i) a.c_s[i] = cache->stride[i];
   a.out = out->data;
   a.o_s0 = out->stride[0]; a.o_s1 = out->stride[1]; a.o_s2 = out->stride[2];
-  a.positions = batch->query_positions;
-  a.cstarts = batch->query_context_start_positions;
-  a.qsl = batch->query_start_locations;
-  a.lengths = batch->context_lengths;
-  a.table = batch->block_table;
-  a.t_s0 = batch->block_table_stride[0];
-  a.t_s1 = batch->block_table_stride[1];
-  a.width = batch->block_table_width;
-  a.num_tokens = N;
-  a.num_requests = batch->num_requests;
-  a.num_blocks = cache->num_blocks;
-  a.block_size = cache->block_size;
-  a.num_q_heads = static_cast<int32_t>(Hq);
-  a.num_kv_heads = static_cast<int32_t>(Hkv);
-  a.group = static_cast<int32_t>(Hq / Hkv);
-  a.head_dim = static_cast<int32_t>(D);
   a.scale_log2 = scale * 1.4426950408889634f;  // log2(e)
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
   const int64_t es = dtype_bytes(dtype);
-  const bool fast = (dtype == MVLLM_DTYPE_BF16 || dtype == MVLLM_DTYPE_F16) && D == 128 &&
-                    a.group <= 16 && cache->stride[4] == 1 && cache->stride[3] == D &&
-                    vec16(cache->stride[0], es) && vec16(cache->stride[1], es) &&
-                    vec16(cache->stride[2], es) && aligned16(cache->data) &&
-                    query->stride[2] == 1 && vec16(query->stride[0], es) &&
+  const bool fast = fast_cache(cache, a.group) && query->stride[2] == 1 && vec16(query->stride[0], es) &&
                     vec16(query->stride[1], es) && aligned16(query->data) && out->stride[2] == 1 &&
                     vec16(out->stride[0], es) && vec16(out->stride[1], es) && aligned16(out->data);
   if (!fast || a.num_requests == 0) {
     a.mode = 0;
     return launch_generic(a, dtype, s);
   }
-  const DecodeLayout d = decode_layout(batch, Hq, D);
-  if (workspace_bytes < d.total() || (!workspace && d.total() > 0))
-    return fail(MVLLM_ERR_WORKSPACE, "workspace of %lld bytes is smaller than the %lld required",
-                (long long)workspace_bytes, (long long)d.total());
-  if (!aligned16(workspace)) return fail(MVLLM_ERR_INVALID, "workspace must be 16-byte aligned");
-  a.split_tokens = d.split_tokens;
-  a.max_splits = d.max_splits;
-  a.ws_acc = static_cast<float*>(workspace);
-  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + d.acc_bytes);
-  a.items = reinterpret_cast<PrefillItem*>(static_cast<char*>(workspace) + d.acc_bytes + d.ml_bytes);
-  a.decode_items = reinterpret_cast<DecodeItem*>(static_cast<char*>(workspace) + d.acc_bytes + d.ml_bytes + d.items_bytes);
+  if (int rc = bind_workspace(a, batch, Hq, D, workspace, workspace_bytes)) return rc;
+  a.lists_ready = planned ? 1 : 0;
   hipEvent_t ds = timing ? static_cast<hipEvent_t>(timing->decode_start) : nullptr;
   hipEvent_t de = timing ? static_cast<hipEvent_t>(timing->decode_stop) : nullptr;
   hipEvent_t ps = timing ? static_cast<hipEvent_t>(timing->prefill_start) : nullptr;
@@ -232,6 +273,22 @@ extern "C" int mvllm_paged_attention(const mvllm_tensor3* query, const mvllm_kv_
   clear_error();
   return paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, nullptr,
                          stream);
+}
+
+extern "C" int mvllm_attention_plan(const mvllm_batch* batch, int64_t num_q_heads,
+                                    const mvllm_kv_cache* cache, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return attention_plan(batch, num_q_heads, cache, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mvllm_paged_attention_planned(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
+                                             const mvllm_batch* batch, const mvllm_tensor3* out,
+                                             float scale, void* workspace, int64_t workspace_bytes,
+                                             void* stream) {
+  clear_error();
+  return paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, nullptr, stream,
+                         true);
 }
 
 extern "C" int mvllm_attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,

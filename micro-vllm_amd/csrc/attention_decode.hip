@@ -25,7 +25,8 @@
 // context fits one split writes its output directly. The combine kernel
 // merges partials with the standard log-sum-exp rescaling (FlashAttention-2,
 // Dao 2023; flash-decoding, Dao et al. 2023) and zero-fills tokens that
-// belong to no request.
+// belong to no request. It learns each request's query token and split count
+// from a table that the work-list kernel writes, one load per workgroup.
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -144,7 +145,11 @@ __global__ __launch_bounds__(512) void decode_split_kernel(AttnArgs a) {
   const int64_t lo = item.lo;
   const int64_t begin = item.begin;
   const int64_t end = item.end;
-  if (begin > end) return;
+  // Records index the query, the table and the partials: out-of-range
+  // fields (never written by the work-list kernel) end the workgroup.
+  if (begin < 0 || begin > end || end - begin >= a.split_tokens || end >= a.width * a.block_size ||
+      qs < 0 || qs >= a.num_tokens || split < 0 || split >= a.max_splits)
+    return;
 
   // Q^T as the B operand: lane (col, grp) holds head col, dims 32i + 8grp .. +8.
   const int G = a.group;
@@ -299,7 +304,11 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
   const int64_t lo = item.lo;
   const int64_t begin = item.begin;
   const int64_t end = item.end;
-  if (begin < 0 || begin > end) return;
+  // Records index the query, the table and the partials: out-of-range
+  // fields (never written by the work-list kernel) end the workgroup.
+  if (begin < 0 || begin > end || end - begin >= a.split_tokens || end >= a.width * a.block_size ||
+      qs < 0 || qs >= a.num_tokens || split < 0 || split >= a.max_splits)
+    return;
   const int ntiles = static_cast<int>((end - begin) / 16 + 1);  // <= 128 (split <= 2048)
 
   // Block id and in-block row of tiles `lane` and `lane + 64` of this split,
@@ -499,12 +508,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
   const int64_t r = blockIdx.x / head_groups;
   const int hq = static_cast<int>(blockIdx.x % head_groups) * kCombineHeads + (threadIdx.x >> 5);
   if (hq >= a.num_q_heads) return;
-  const int64_t qs = a.qsl[r];
-  if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return;
-  int64_t lo, hi;
-  visible_range(a, r, qs, qs, lo, hi);
-  const int64_t ns = decode_num_splits(lo, hi, a.split_tokens);
-  if (ns == 1) return;
+  // (query token, splits) from the work-list kernel: -1 is not a decode
+  // request, and a single split has written its output itself.
+  const int2 req = a.decode_req[r];
+  const int64_t qs = req.x, ns = req.y;
+  if (ns < 0 || ns == 1 || ns > a.max_splits || qs < 0 || qs >= a.num_tokens) return;
   const int d0 = (threadIdx.x & 31) * 4;
   uint32_t w[2];
   if (ns == 0) {
@@ -582,19 +590,21 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   if (tid == 0) full_count = full_pos = 0;
   if (tid < kSizeBuckets) bucket[tid] = 0;
   // A decode request: its query token, visible keys, split count and the
-  // size of its last split (ns = 0: not a decode request).
+  // size of its last split (ns = 0: not a decode request, or no visible key;
+  // dec = 1 marks a decode request).
   struct Desc {
-    int32_t qs, lo, hi, ns, last;
+    int32_t qs, lo, hi, ns, last, dec;
   };
   auto describe = [&](int64_t r) {
-    Desc d = {0, 0, -1, 0, 0};
+    Desc d = {0, 0, -1, 0, 0, 0};
     const int64_t qs = a.qsl[r];
     if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return d;
+    d.qs = static_cast<int32_t>(qs);
+    d.dec = 1;
     int64_t lo, hi;
     visible_range(a, r, qs, qs, lo, hi);
     const int64_t n = decode_num_splits(lo, hi, a.split_tokens);
     if (n <= 0) return d;
-    d.qs = static_cast<int32_t>(qs);
     d.lo = static_cast<int32_t>(lo);
     d.hi = static_cast<int32_t>(hi);
     d.ns = static_cast<int32_t>(n);
@@ -607,7 +617,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
     return DecodeItem{static_cast<int32_t>(r), sp, d.qs, d.ns, d.lo, d.hi, begin, end};
   };
   // The thread's first request stays in registers between the passes.
-  Desc d0 = {0, 0, -1, 0, 0};
+  Desc d0 = {0, 0, -1, 0, 0, 0};
   if (tid < R) d0 = describe(tid);
   __syncthreads();
   const int lane = tid & 63;
@@ -626,7 +636,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   // partial ones by size. The loop bound is uniform per wave.
   for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
     const int64_t r = r0 + lane;
-    Desc d = {0, 0, -1, 0, 0};
+    Desc d = {0, 0, -1, 0, 0, 0};
     if (r < R) d = r == tid ? d0 : describe(r);
     const int32_t ns = d.ns, last = d.last;
     const bool partial = ns > 0 && last < a.split_tokens;
@@ -655,7 +665,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   // Pass 2: place the items (one LDS atomic per wave for the full splits).
   for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
     const int64_t r = r0 + lane;
-    Desc d = {0, 0, -1, 0, 0};
+    Desc d = {0, 0, -1, 0, 0, 0};
     if (r < R) d = r == tid ? d0 : describe(r);
     const int32_t ns = d.ns, last = d.last;
     const bool partial = ns > 0 && last < a.split_tokens;
@@ -667,6 +677,7 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
     at = __shfl(at, 0, 64) + excl;
     for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = record(r, d, sp);
     if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> bucket_shift], 1)] = record(r, d, ns - 1);
+    if (r < R) a.decode_req[r] = int2{d.qs, d.dec ? ns : -1};
   }
   for (int64_t j = full_count + tid; j < capacity; j += kDecodeListThreads)
     a.decode_items[j] = DecodeItem{-1, -1, 0, 0, 0, -1, 0, -1};
@@ -733,12 +744,11 @@ int launch_decode_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent
   if (a.num_requests > 0) {
     const int64_t blocks = a.num_requests * a.max_splits * groups;
     if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "decode grid too large (%lld workgroups)", (long long)blocks);
-    if (!a.decode_items) return fail(MVLLM_ERR_INVALID, "decode work list is missing");
-    // Work-list records carry positions and token indices as int32.
-    if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX)
+    if (!a.lists_ready) {
+      if (int rc = launch_decode_lists(a, s)) return rc;
+    } else if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX) {
       return fail(MVLLM_ERR_UNSUPPORTED, "decode positions beyond 2^31 are not supported");
-    hipLaunchKernelGGL(decode_items_kernel, dim3(1), dim3(kDecodeListThreads), 0, s, a);
-    MVLLM_LAUNCH_CHECK("decode_items_kernel");
+    }
     const dim3 grid(static_cast<unsigned>(blocks));
     const dim3 block(64 * waves);
     if (tune.lds_pipeline) {
@@ -771,6 +781,17 @@ int launch_decode_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent
 }
 
 }  // namespace
+
+int launch_decode_lists(const AttnArgs& a, hipStream_t s) {
+  if (a.num_requests <= 0) return MVLLM_OK;
+  if (!a.decode_items || !a.decode_req) return fail(MVLLM_ERR_INVALID, "decode work list is missing");
+  // Work-list records carry positions and token indices as int32.
+  if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX)
+    return fail(MVLLM_ERR_UNSUPPORTED, "decode positions beyond 2^31 are not supported");
+  hipLaunchKernelGGL(decode_items_kernel, dim3(1), dim3(kDecodeListThreads), 0, s, a);
+  MVLLM_LAUNCH_CHECK("decode_items_kernel");
+  return MVLLM_OK;
+}
 
 int launch_decode(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t start,
                   hipEvent_t stop) {

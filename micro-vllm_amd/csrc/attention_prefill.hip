@@ -178,7 +178,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   const int64_t t1 = item.t1;
   if (qs < 0 || t0 < qs || t0 >= t1 || t1 > a.num_tokens) return;
   const int32_t hull_lo = item.lo, hull_hi = item.hi;
-  const bool hull_ok = hull_hi >= hull_lo;
+  // The hull bounds the page-table fill below: keep it inside the table.
+  const bool hull_ok = hull_hi >= hull_lo && hull_lo >= 0 && hull_hi < a.width * a.block_size;
   const int32_t hull_base = hull_ok ? (hull_lo & ~15) : 0;
   const int32_t hull_tiles = hull_ok ? (hull_hi - hull_base) / kTileKeys + 1 : 0;
 
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   // Rows inside the hull (always, when ranges grow with the token): keys
   // [hull_lo, hull_hi], whose first chunk of block ids is already in LDS.
   // Otherwise the rows' own bounds, and the table is fetched again.
-  const bool hull_table = kmax >= kmin && kmin >= hull_lo && kmax <= hull_hi;
+  const bool hull_table = hull_ok && kmax >= kmin && kmin >= hull_lo && kmax <= hull_hi;
   if (hull_table) {
     kmin = hull_lo;
     kmax = hull_hi;
@@ -659,17 +660,25 @@ __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a,
   for (int64_t j = total + tid; j < nslots; j += kItemThreads) a.items[j] = empty;
 }
 
+// T = kRows / G query tokens per work item.
+int prefill_lg_tok(const AttnArgs& a) {
+  int lg_tok = 0;
+  while ((kRows >> lg_tok) > a.group) ++lg_tok;
+  return lg_tok;
+}
+
 template <typename T, bool PSPLIT>
 int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
-  int lg_tok = 0;
-  while ((kRows >> lg_tok) > a.group) ++lg_tok;  // T = kRows / G
+  const int lg_tok = prefill_lg_tok(a);
   const int64_t nblk = a.num_tokens / (int64_t{1} << lg_tok) + a.num_requests;
   const int64_t blocks = nblk * a.num_kv_heads;
   if (blocks <= 0) return MVLLM_OK;
   if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "prefill grid too large");
   if (!a.items) return fail(MVLLM_ERR_INVALID, "prefill work list is missing");
-  prefill_items_kernel<<<1, kItemThreads, 0, s>>>(a, lg_tok);
-  MVLLM_LAUNCH_CHECK("prefill_items_kernel");
+  if (!a.lists_ready) {
+    prefill_items_kernel<<<1, kItemThreads, 0, s>>>(a, lg_tok);
+    MVLLM_LAUNCH_CHECK("prefill_items_kernel");
+  }
   static bool raised = false;  // per instantiation; the attribute is process-wide
   if (!raised) {
     MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<T, PSPLIT>),
@@ -684,6 +693,17 @@ int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEven
 }
 
 }  // namespace
+
+int launch_prefill_lists(const AttnArgs& a, hipStream_t s) {
+  const int lg_tok = prefill_lg_tok(a);
+  const int64_t blocks = (a.num_tokens / (int64_t{1} << lg_tok) + a.num_requests) * a.num_kv_heads;
+  if (blocks <= 0) return MVLLM_OK;
+  if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "prefill grid too large");
+  if (!a.items) return fail(MVLLM_ERR_INVALID, "prefill work list is missing");
+  prefill_items_kernel<<<1, kItemThreads, 0, s>>>(a, lg_tok);
+  MVLLM_LAUNCH_CHECK("prefill_items_kernel");
+  return MVLLM_OK;
+}
 
 bool prefill_supported(const AttnArgs& a, int32_t dtype) {
   if (dtype != MVLLM_DTYPE_BF16 && dtype != MVLLM_DTYPE_F16) return false;

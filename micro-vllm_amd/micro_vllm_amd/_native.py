@@ -16,7 +16,7 @@ import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libmvllm_amd.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "mvllm_kv_write",
     "mvllm_attention_workspace_bytes",
     "mvllm_paged_attention",
+    "mvllm_attention_plan",
+    "mvllm_paged_attention_planned",
     "mvllm_attention_forward",
     "mvllm_attention_forward_timed",
     "mvllm_gather_kv",
@@ -154,6 +156,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         p(Tensor3), p(KVCache), p(Batch), p(Tensor3), ctypes.c_float, _ptr, _i64, _ptr,
     ]
     lib.mvllm_paged_attention.restype = ctypes.c_int
+    lib.mvllm_attention_plan.argtypes = [p(Batch), _i64, p(KVCache), _ptr, _i64, _ptr]
+    lib.mvllm_attention_plan.restype = ctypes.c_int
+    lib.mvllm_paged_attention_planned.argtypes = [
+        p(Tensor3), p(KVCache), p(Batch), p(Tensor3), ctypes.c_float, _ptr, _i64, _ptr,
+    ]
+    lib.mvllm_paged_attention_planned.restype = ctypes.c_int
     lib.mvllm_attention_forward.argtypes = [
         p(Tensor3), p(Tensor3), p(Tensor3), p(KVCache), p(Batch), p(Tensor3),
         ctypes.c_float, _ptr, _i64, _ptr,

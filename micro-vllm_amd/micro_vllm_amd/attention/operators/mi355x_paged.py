@@ -174,27 +174,70 @@ def hip_paged_attention(
     return output
 
 
+class AttentionPlan:
+    """Work lists of one batch, built once and shared by every layer of a step.
+
+    The reference's operator runs per layer (qwen.py:89-99); the lists depend
+    only on the batch, so a model whose layers share one metadata bundle and
+    one cache geometry plans once per step (``mvllm_attention_plan``) and
+    each layer's ``hip_attention_over_cache(..., plan=plan)`` skips the
+    list kernels. The plan owns the workspace, which every planned call on
+    the same stream reuses for its split-KV partials.
+    """
+
+    def __init__(self, metadata: AttentionMetadata, num_q_heads: int, layer_kv_cache: torch.Tensor):
+        device = layer_kv_cache.device
+        if device.type != "cuda":
+            raise RuntimeError("mi355x_paged attention plans require a GPU cache")
+        self.metadata = metadata
+        self.num_q_heads = num_q_heads
+        self.batch, self._keep = batch_descriptor(metadata, device)
+        lib = _native.load()
+        head_dim = layer_kv_cache.shape[-1]
+        nbytes = lib.mvllm_attention_workspace_bytes(self.batch, num_q_heads, head_dim)
+        self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _native.check(
+            lib.mvllm_attention_plan(
+                self.batch,
+                num_q_heads,
+                _native.kv_cache(layer_kv_cache),
+                self.workspace.data_ptr(),
+                self.workspace.numel(),
+                _native.stream_handle(device),
+            ),
+            "mvllm_attention_plan",
+        )
+
+
 def hip_attention_over_cache(
     query: torch.Tensor,
     layer_kv_cache: torch.Tensor,
     metadata: AttentionMetadata,
+    plan: AttentionPlan | None = None,
 ) -> torch.Tensor:
     """Ragged causal attention over a cache that already holds the step's
     K/V (written by ``layers.qk_norm_rope_kv_write``): the attention part of
-    ``hip_paged_attention``, without the cache write."""
+    ``hip_paged_attention``, without the cache write. With ``plan`` (made for
+    this metadata and head count) the work lists are not rebuilt."""
 
     if query.device.type != "cuda" or layer_kv_cache.device != query.device:
         raise RuntimeError("mi355x_paged attention requires GPU tensors on one device")
     if query.dtype not in SUPPORTED_DTYPES or layer_kv_cache.dtype != query.dtype:
         raise ValueError(f"unsupported or mismatched dtypes {query.dtype} / {layer_kv_cache.dtype}")
     device = query.device
-    batch, keep = batch_descriptor(metadata, device)
     output = torch.empty_like(query)
     lib = _native.load()
-    workspace_bytes = lib.mvllm_attention_workspace_bytes(batch, query.shape[1], query.shape[2])
-    workspace = torch.empty(max(workspace_bytes, 1), dtype=torch.uint8, device=device)
+    if plan is not None:
+        if plan.metadata is not metadata or plan.num_q_heads != query.shape[1]:
+            raise ValueError("attention plan was made for other metadata or another head count")
+        batch, keep, workspace, entry = plan.batch, None, plan.workspace, "mvllm_paged_attention_planned"
+    else:
+        batch, keep = batch_descriptor(metadata, device)
+        workspace_bytes = lib.mvllm_attention_workspace_bytes(batch, query.shape[1], query.shape[2])
+        workspace = torch.empty(max(workspace_bytes, 1), dtype=torch.uint8, device=device)
+        entry = "mvllm_paged_attention"
     _native.check(
-        lib.mvllm_paged_attention(
+        getattr(lib, entry)(
             _native.tensor3(query),
             _native.kv_cache(layer_kv_cache),
             batch,
@@ -204,7 +247,7 @@ def hip_attention_over_cache(
             workspace.numel(),
             _native.stream_handle(device),
         ),
-        "mvllm_paged_attention",
+        entry,
     )
     del keep
     return output

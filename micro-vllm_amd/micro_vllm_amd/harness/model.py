@@ -219,7 +219,7 @@ class DecoderModel:
         metadata: AttentionMetadata,
     ) -> torch.Tensor:
         from micro_vllm_amd import layers
-        from micro_vllm_amd.attention.operators.mi355x_paged import hip_attention_over_cache
+        from micro_vllm_amd.attention.operators.mi355x_paged import AttentionPlan, hip_attention_over_cache
 
         c = self.config
         eps = c.rms_norm_eps
@@ -231,6 +231,8 @@ class DecoderModel:
         sine = sine.reshape(n, c.head_dim).contiguous()
         residual = F.embedding(input_ids, self.embed)
         x = layers.add_rms_norm(residual, self.layers[0]["input_norm"], eps)
+        # Every layer sees the same batch: its work lists are built once.
+        plan = AttentionPlan(metadata, c.num_attention_heads, kv_caches[0])
         for i, (layer, cache) in enumerate(zip(self.layers, kv_caches)):
             qkv = F.linear(x, layer["qkv"])
             q = qkv[:, :q_size].view(n, c.num_attention_heads, c.head_dim)
@@ -248,7 +250,7 @@ class DecoderModel:
                 cache,
                 metadata.slot_mapping,
             )
-            attention = hip_attention_over_cache(q, cache, metadata)
+            attention = hip_attention_over_cache(q, cache, metadata, plan=plan)
             x = layers.add_rms_norm(F.linear(attention.flatten(1), layer["o"]), layer["post_norm"], eps, residual)
             mlp = F.linear(layers.silu_mul(F.linear(x, layer["gate_up"])), layer["down"])
             next_norm = self.layers[i + 1]["input_norm"] if i + 1 < len(self.layers) else self.final_norm

@@ -341,6 +341,46 @@ def test_prefill_kernel_rows_outside_the_work_list_hull(device, hq, hkv):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
+PLAN_CASES = {
+    "mixed": ([300, 1000, 17, 2049, 600, 5], [300, 1, 17, 1, 64, 1]),
+    "decode": ([129, 4100, 700, 16, 33, 2500], [1] * 6),
+    "prefill": ([600, 90, 2100], [600, 90, 48]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(PLAN_CASES))
+def test_planned_attention_matches_per_call_lists(device, case):
+    """One plan (work lists built once) serves three layers whose caches share
+    the geometry but not the contents: every planned call equals the call
+    that builds its own lists, bit for bit."""
+
+    from micro_vllm_amd.attention.operators.mi355x_paged import AttentionPlan, hip_attention_over_cache
+
+    lengths, qlens = PLAN_CASES[case]
+    dtype = torch.bfloat16
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, 32, 8, 128, 16, seed=67, nan_cache=False)
+    operator()(q, k, v, cache, md)  # writes the step's K/V
+    caches = [cache, cache * 0.5, cache.flip(1).contiguous()]
+    plan = AttentionPlan(md, 32, caches[0])
+    for layer_cache in caches:
+        planned = hip_attention_over_cache(q, layer_cache, md, plan=plan)
+        direct = hip_attention_over_cache(q, layer_cache, md)
+        torch.cuda.synchronize()
+        assert torch.equal(planned.view(torch.int16), direct.view(torch.int16))
+
+
+def test_plan_for_other_metadata_is_rejected(device):
+    from micro_vllm_amd.attention.operators.mi355x_paged import AttentionPlan, hip_attention_over_cache
+
+    q, k, v, cache, md = build_case(device, torch.bfloat16, [40, 7], [40, 1], 16, 8, 128, 16, seed=71)
+    _, _, _, _, md2 = build_case(device, torch.bfloat16, [40, 7], [40, 1], 16, 8, 128, 16, seed=71)
+    plan = AttentionPlan(md, 16, cache)
+    with pytest.raises(ValueError):
+        hip_attention_over_cache(q, cache, md2, plan=plan)
+    with pytest.raises(ValueError):
+        hip_attention_over_cache(q[:, :8].contiguous(), cache, md, plan=plan)
+
+
 def test_prefill_kernel_reloads_page_table_on_long_context(device):
     """A 40,000-key visible range spans more than one LDS page-table load
     (2,048 pages)."""
