@@ -519,6 +519,39 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
     // Nothing visible: softmax over no keys is NaN in the reference.
     const uint32_t nan_bits = Elem<T>::to_bits(NAN);
     w[0] = w[1] = nan_bits | (nan_bits << 16);
+  } else if (ns <= 8) {
+    // Up to eight splits (the common case): every split's (max, sum) and
+    // accumulator slice are loaded at once, one round trip after the table.
+    const int sub = threadIdx.x & 31;
+    const int64_t first_item = r * a.max_splits * a.num_q_heads + hq;
+    const int cnt = static_cast<int>(ns);
+    float2 ml = make_float2(-INFINITY, 0.f);
+    if (sub < cnt) ml = a.ws_ml[first_item + sub * a.num_q_heads];
+    const float* accp = a.ws_acc + first_item * kDim + d0;
+    float4_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = j < cnt ? j : cnt - 1;  // indices past the last split re-read it, unused
+      v[j] = *reinterpret_cast<const float4_t*>(accp + static_cast<int64_t>(k) * a.num_q_heads * kDim);
+    }
+    float mx = ml.x;  // lanes past the last split hold -inf and a zero sum
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 32));
+    // A split with no visible key (m = -inf) weighs 0; so does every split
+    // when none has one, and the output is then NaN (0 / 0).
+    const float wgt = ml.x == -INFINITY ? 0.f : exp2f(ml.x - mx);
+    float sum = wgt * ml.y;
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 32);
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float wj = __shfl(wgt, j, 32);
+      if (j < cnt) o += v[j] * wj;
+    }
+    const float inv = 1.f / sum;
+    w[0] = Elem<T>::to_bits(o[0] * inv) | (Elem<T>::to_bits(o[1] * inv) << 16);
+    w[1] = Elem<T>::to_bits(o[2] * inv) | (Elem<T>::to_bits(o[3] * inv) << 16);
   } else {
     // Two passes over the head's splits, 32 lanes wide: the maximum first,
     // then every split's weight exp2(m_s - max) from its own lane, so the
