@@ -70,6 +70,9 @@ def test_library_rejects_bad_arguments_without_a_device():
     assert b"spec" in lib.mvllm_last_error()
     assert lib.mvllm_kv_write(None, None, None, None, 0, None) == _native.ERR_INVALID
     assert lib.mvllm_attention_workspace_bytes(None, 16, 128) == 0
+    assert lib.mvllm_attention_plan(None, 16, None, None, 0, None) == _native.ERR_INVALID
+    assert b"cache" in lib.mvllm_last_error()
+    assert lib.mvllm_paged_attention_planned(None, None, None, None, 1.0, None, 0, None) == _native.ERR_INVALID
 
 
 def test_registry_returns_the_hip_operator():
