@@ -123,6 +123,48 @@ extern "C" int64_t mvllm_attention_workspace_bytes(const mvllm_batch* batch, int
 namespace mvllm {
 namespace {
 
+// A second stream per device for the prefill launch of a mixed batch: the
+// MFMA-bound prefill kernel then runs beside the HBM-bound decode kernel
+// instead of after it (a CU holds one workgroup of each). Default priority,
+// non-blocking; created on the first eager call and never destroyed. The
+// caller's stream forks to it after the KV write and joins it before the
+// call returns, so the call behaves like one launch sequence on the
+// caller's stream (and a graph capture records two branches). Calls are
+// expected from one host thread at a time per device, as the operator's.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+SideStream* side_stream(hipStream_t caller) {
+  if (const char* env = std::getenv("MVLLM_PREFILL_CONCURRENT"))
+    if (std::atoi(env) == 0) return nullptr;
+  static std::mutex mu;
+  static SideStream per_device[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  SideStream& ss = per_device[dev];
+  if (!ss.stream) {
+    // Creating streams or events during a graph capture may be refused:
+    // such a call stays on the caller's stream.
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(caller, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return nullptr;
+    hipStream_t st = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      (void)hipStreamDestroy(st);
+      return nullptr;
+    }
+    ss.stream = st;
+    ss.fork = f;
+    ss.join = j;
+  }
+  return &ss;
+}
+
 // Batch and cache fields of the kernel arguments.
 void fill_batch_args(AttnArgs& a, const mvllm_batch* batch, const mvllm_kv_cache* cache, int64_t Hq) {
   a.cache = cache->data;
@@ -240,10 +282,27 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
   hipEvent_t de = timing ? static_cast<hipEvent_t>(timing->decode_stop) : nullptr;
   hipEvent_t ps = timing ? static_cast<hipEvent_t>(timing->prefill_start) : nullptr;
   hipEvent_t pe = timing ? static_cast<hipEvent_t>(timing->prefill_stop) : nullptr;
-  if (int rc = launch_decode(a, dtype, s, ds, de)) return rc;
   // A batch known to hold only single-query requests needs no prefill launch.
+  if (batch->max_query_len != 1 && prefill_supported(a, dtype)) {
+    SideStream* side = side_stream(s);
+    hipStream_t pst = s;
+    if (side) {
+      MVLLM_HIP_TRY(hipEventRecord(side->fork, s));
+      MVLLM_HIP_TRY(hipStreamWaitEvent(side->stream, side->fork, 0));
+      pst = side->stream;
+    }
+    // The prefill goes first so that its workgroups are queued before the
+    // decode grid fills the chip. Both branches are joined even on error.
+    int rc = launch_prefill(a, dtype, pst, ps, pe);
+    if (rc == MVLLM_OK) rc = launch_decode(a, dtype, s, ds, de);
+    if (side) {
+      MVLLM_HIP_TRY(hipEventRecord(side->join, side->stream));
+      MVLLM_HIP_TRY(hipStreamWaitEvent(s, side->join, 0));
+    }
+    return rc;
+  }
+  if (int rc = launch_decode(a, dtype, s, ds, de)) return rc;
   if (batch->max_query_len == 1) return MVLLM_OK;
-  if (prefill_supported(a, dtype)) return launch_prefill(a, dtype, s, ps, pe);
   a.mode = 1;
   return launch_generic(a, dtype, s);
 }

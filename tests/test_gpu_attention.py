@@ -369,6 +369,20 @@ def test_planned_attention_matches_per_call_lists(device, case):
         assert torch.equal(planned.view(torch.int16), direct.view(torch.int16))
 
 
+def test_prefill_beside_decode_matches_serial_step(device, monkeypatch):
+    """A mixed batch runs its prefill kernel on a second stream beside the
+    decode kernel; the outputs must equal the serial step's bit for bit, and
+    the oracle's within tolerance."""
+
+    lengths = [300, 1000, 17, 2049, 600, 5, 4000]
+    qlens = [300, 1, 17, 1, 64, 1, 1]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 32, 8, 128, 16, seed=73)
+    overlapped = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
+    monkeypatch.setenv("MVLLM_PREFILL_CONCURRENT", "0")
+    serial = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
+    assert torch.equal(overlapped.view(torch.int16), serial.view(torch.int16))
+
+
 def test_plan_for_other_metadata_is_rejected(device):
     from micro_vllm_amd.attention.operators.mi355x_paged import AttentionPlan, hip_attention_over_cache
 
