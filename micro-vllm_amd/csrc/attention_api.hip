@@ -141,8 +141,10 @@ SideStream* side_stream(hipStream_t caller) {
     if (std::atoi(env) == 0) return nullptr;
   static std::mutex mu;
   static SideStream per_device[64];
+  // The caller's stream decides the device (the null stream: the current one).
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (caller ? hipStreamGetDevice(caller, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= 64) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
   SideStream& ss = per_device[dev];
   if (!ss.stream) {
@@ -150,12 +152,18 @@ SideStream* side_stream(hipStream_t caller) {
     // such a call stays on the caller's stream.
     hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(caller, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return nullptr;
+    int current = 0;
+    if (hipGetDevice(&current) != hipSuccess) return nullptr;
+    if (current != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
     hipStream_t st = nullptr;
     hipEvent_t f = nullptr, j = nullptr;
-    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-      (void)hipStreamDestroy(st);
+    bool ok = hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess;
+    ok = ok && hipEventCreateWithFlags(&f, hipEventDisableTiming) == hipSuccess;
+    ok = ok && hipEventCreateWithFlags(&j, hipEventDisableTiming) == hipSuccess;
+    if (current != dev) (void)hipSetDevice(current);
+    if (!ok) {
+      if (st) (void)hipStreamDestroy(st);
+      if (f) (void)hipEventDestroy(f);
       return nullptr;
     }
     ss.stream = st;
