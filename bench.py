@@ -422,7 +422,7 @@ def main() -> int:
 
     if args.gpus != 1:
         print(
-            f"bench.py runs on one GPU: --gpus {args.gpus} is not supported by this build "
+            f"bench.py runs on one GPU: --gpus {args.gpus} is not supported "
             "(the multi-GPU sharding of the path is described, not implemented).",
             file=sys.stderr,
         )

@@ -50,7 +50,7 @@ enum {
 enum {
   MVLLM_OK = 0,
   MVLLM_ERR_INVALID = -1,     /* bad shape, stride, pointer or size */
-  MVLLM_ERR_UNSUPPORTED = -2, /* dtype / geometry this build does not handle */
+  MVLLM_ERR_UNSUPPORTED = -2, /* dtype / geometry the library does not handle */
   MVLLM_ERR_HIP = -3,         /* a HIP runtime call failed */
   MVLLM_ERR_WORKSPACE = -4    /* workspace smaller than required */
 };
