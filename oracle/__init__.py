@@ -2,7 +2,8 @@
 
 A numpy restatement of the reference's attention operator and packing code,
 used only by ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` as the checker. The HIP library never imports it.
+leg of ``bench.py``, as the reference results the HIP path is compared with.
+The HIP library never imports it.
 
 Every function is pinned against the reference tests' literal vectors and
 against closed forms in ``tests/test_oracle.py``; none is left unpinned.

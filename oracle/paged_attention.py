@@ -1,8 +1,8 @@
 """CPU oracle for micro-vLLM's ragged paged attention (TEST INFRASTRUCTURE ONLY).
 
 This module restates, in numpy, what the reference's
-``ReferenceAttentionOperator`` computes. It is the checker that the HIP
-library is compared against: only ``tests/``, ``__graft_entry__.smoke()`` and
+``ReferenceAttentionOperator`` computes. The HIP library's results are
+compared with it: only ``tests/``, ``__graft_entry__.smoke()`` and
 the ``cpu_baseline`` leg of ``bench.py`` may import it, and never as the thing
 that is measured or shipped.
 

@@ -3,7 +3,7 @@
 * ``gpu`` marks tests that need a visible GPU (run with ``-m gpu``).
 * The package lives under ``micro-vllm_amd/`` (not importable by that name),
   so its parent directory is put on ``sys.path``; the repository root is on
-  it too, for the oracle (the checker).
+  it too, for the oracle.
 """
 
 from __future__ import annotations

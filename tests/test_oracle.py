@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (the checker) before it is trusted.
+"""Pins the CPU oracle before it is trusted.
 
 Each oracle function is checked against something independent of its own
 formula:
