@@ -1,5 +1,5 @@
-"""A torch (GPU) restatement of the reference attention operator, used as the
-checker of end-to-end greedy decoding (TEST INFRASTRUCTURE ONLY).
+"""A torch (GPU) restatement of the reference attention operator, against
+which end-to-end greedy decoding is compared (TEST INFRASTRUCTURE ONLY).
 
 Same semantics as ReferenceAttentionOperator.forward
 (src/micro_vllm/attention/operators/reference.py:14-138): write the step's
