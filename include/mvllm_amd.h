@@ -14,11 +14,11 @@
  *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *    Calls only enqueue work: nothing synchronises with the host, no device
  *    memory is allocated, so every entry point may be recorded into a HIP
- *    graph. The attention entry points run a mixed batch's prefill kernel
- *    on a second, library-owned stream (one per device, default priority,
- *    created by the first call made outside a graph capture), forked from
- *    and joined back into `stream` within the call;
- *    MVLLM_PREFILL_CONCURRENT=0 keeps all work on `stream`.
+ *    graph. When mvllm_batch.max_query_len > 1, the attention entry points
+ *    run the prefill kernel on a second, library-owned stream (one per
+ *    device, default priority, created by the first call made outside a
+ *    graph capture), forked from and joined back into `stream` within the
+ *    call; MVLLM_PREFILL_CONCURRENT=0 keeps all work on `stream`.
  *  - Return value: 0 on success, a negative MVLLM_ERR_* code on failure;
  *    mvllm_last_error() then describes the failure (thread-local text).
  *  - Index tensors are int64, as in the reference (AttentionMetadata,

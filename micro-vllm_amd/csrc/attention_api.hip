@@ -292,7 +292,9 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
   hipEvent_t pe = timing ? static_cast<hipEvent_t>(timing->prefill_stop) : nullptr;
   // A batch known to hold only single-query requests needs no prefill launch.
   if (batch->max_query_len != 1 && prefill_supported(a, dtype)) {
-    SideStream* side = side_stream(s);
+    // A fork and join cost ~10 us: the prefill moves to the side stream only
+    // when the hint says that the batch holds multi-query requests.
+    SideStream* side = batch->max_query_len > 1 ? side_stream(s) : nullptr;
     hipStream_t pst = s;
     if (side) {
       MVLLM_HIP_TRY(hipEventRecord(side->fork, s));

@@ -13,6 +13,7 @@ check of the 256-sequence Qwen3 decode batch, and graph replay.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 
 import numpy as np
@@ -377,6 +378,7 @@ def test_prefill_beside_decode_matches_serial_step(device, monkeypatch):
     lengths = [300, 1000, 17, 2049, 600, 5, 4000]
     qlens = [300, 1, 17, 1, 64, 1, 1]
     q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 32, 8, 128, 16, seed=73)
+    md = dataclasses.replace(md, max_query_len=max(qlens))  # the hint that enables the second stream
     overlapped = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
     monkeypatch.setenv("MVLLM_PREFILL_CONCURRENT", "0")
     serial = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
@@ -500,6 +502,9 @@ def test_qwen3_decode_batch_sampled(device):
 
 def test_graph_replay_matches_eager(device):
     q, k, v, cache, md = build_case(device, torch.bfloat16, [300, 1, 2000, 45], [1, 1, 1, 20], 16, 8, 128, 16, seed=5, nan_cache=False)
+    # With the hint, the prefill runs on the library's second stream, so the
+    # capture holds a fork and a join.
+    md = dataclasses.replace(md, max_query_len=20)
     op = operator()
     eager_cache = cache.clone()
     eager = op(q, k, v, eager_cache, md)
