@@ -392,8 +392,9 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
     const int stage = k % STAGES;
     const int ahead = k + STAGES - 1;
     if (ahead < ntiles) {
-      // The stage being refilled was read two iterations ago; its LDS reads
-      // have completed (their results fed the MFMAs), so it may be overwritten.
+      // The stage being refilled, (k - 1) % STAGES, was read in the previous
+      // iteration. Its LDS reads have retired only because that iteration
+      // ended with an lgkmcnt(0) wait; that wait is what makes the refill safe.
       issue(ahead, ahead % STAGES);
     }
     const int later = (ntiles - 1 - k) < (STAGES - 1) ? (ntiles - 1 - k) : (STAGES - 1);
@@ -611,7 +612,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
 // ends on the shortest items. Empty slots (up to R * max_splits) get
 // request -1.
 constexpr int kDecodeListThreads = 1024;
-constexpr int kSizeBuckets = 64;  // sizes of a partial split, 16 or 32 tokens each (split <= 2048)
+constexpr int kSizeBuckets = 64;  // sizes of a partial split, split / 64 tokens (rounded up to a power of two) each
 
 __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnArgs a) {
   __shared__ int32_t full_count, full_pos;
@@ -619,7 +620,11 @@ __global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnAr
   const int tid = threadIdx.x;
   const int64_t R = a.num_requests;
   const int64_t capacity = R * a.max_splits;
-  const int bucket_shift = a.split_tokens > 1024 ? 5 : 4;  // 64 buckets span the split
+  // 64 buckets of 2^bucket_shift sizes span every split length: the
+  // smallest shift with 64 << shift >= split_tokens (a partial split holds
+  // 1 .. split_tokens - 1 keys, so its bucket index stays below 64).
+  int bucket_shift = 0;
+  while ((kSizeBuckets << bucket_shift) < a.split_tokens) ++bucket_shift;
   if (tid == 0) full_count = full_pos = 0;
   if (tid < kSizeBuckets) bucket[tid] = 0;
   // A decode request: its query token, visible keys, split count and the

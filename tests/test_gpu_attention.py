@@ -537,6 +537,10 @@ DECODE_VARIANTS = [
     {"MVLLM_DECODE_SPLIT": "1024"},
     {"MVLLM_DECODE_SPLIT": "1536"},
     {"MVLLM_DECODE_SPLIT": "2048"},
+    # Longer than the pipelined kernel takes: the general kernel, and the
+    # work list's size buckets scaled to the split (contexts 3000 and 5003
+    # leave partial splits of 2,992 and 911 keys).
+    {"MVLLM_DECODE_SPLIT": "4096"},
 ]
 
 
