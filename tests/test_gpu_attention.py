@@ -463,19 +463,27 @@ def test_prefill_kernel_unmapped_pages_are_masked(device):
     torch.testing.assert_close(out.double().cpu(), expected, **TOL[dtype])
 
 
-def test_llama3_mixed_batch_sampled(device):
+def check_whole_batch(w, out, group=32):
+    """Every request of a large workload against the oracle, ``group``
+    requests at a time (bounded host memory); also that no token outside
+    the requests' rows is NaN."""
+
+    assert not torch.isnan(out).any()
+    requests = list(range(len(w.context_lengths)))
+    for i in range(0, len(requests), group):
+        expected, got = subset_step(w, requests[i : i + group], out)
+        assert_attention_close(got, expected, **TOL[torch.bfloat16])
+
+
+def test_llama3_mixed_batch_whole(device):
     """The Llama-3-head mixed batch (8 chunks of 512 at offsets U[0, 2048] +
-    248 decodes U[256, 8192]): every prefill chunk and a sample of decodes
-    against the oracle."""
+    248 decodes U[256, 8192], 4,344 tokens): every request against the
+    oracle."""
 
     w = workloads.llama3_mixed(device)
     out = operator()(w.query, w.key, w.value, w.cache, w.metadata)
     torch.cuda.synchronize()
-    assert not torch.isnan(out).any()
-    chunks = [r for r in range(len(w.query_lengths)) if w.query_lengths[r] > 1]
-    sample = chunks + [8, 9, 100, 255]
-    expected, got = subset_step(w, sample, out)
-    assert_attention_close(got, expected, **TOL[torch.bfloat16])
+    check_whole_batch(w, out)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -486,18 +494,102 @@ def test_small_mixed_batch(device, dtype):
     run_and_check(w.query, w.key, w.value, w.cache, w.metadata, dtype)
 
 
-def test_qwen3_decode_batch_sampled(device):
+def test_qwen3_decode_batch_whole(device):
     """The 256-sequence Qwen3 decode batch (contexts U[128, 4096], 70k-block
-    pool): 12 sampled requests against the oracle, no NaN anywhere."""
+    pool): every request against the oracle."""
 
     w = workloads.qwen3_decode(device)
     out = operator()(w.query, w.key, w.value, w.cache, w.metadata)
     torch.cuda.synchronize()
-    assert not torch.isnan(out).any()
-    order = np.argsort(w.context_lengths)
-    sample = sorted(set(order[:4].tolist() + order[-4:].tolist() + order[120:124].tolist()))
-    expected, got = subset_step(w, sample, out)
-    assert_attention_close(got, expected, **TOL[torch.bfloat16])
+    check_whole_batch(w, out, group=64)
+
+
+# ------------------------------------------------- shared prefix (prefix cache)
+
+
+def shared_prefix_case(device, prefix_len, plan, hq, hkv, seed, twins=()):
+    """Requests whose block tables start with the same physical blocks (the
+    prefix cache hands a hit's blocks to every request that shares the
+    prefix, kv_cache_manager.py:113-134). ``plan`` lists per request
+    (suffix history length, query length); each request owns the blocks
+    past the prefix. Requests in a pair of ``twins`` get identical suffix
+    history, queries, keys and values. Everything the batch must not read
+    is NaN."""
+
+    bs, d = 16, 128
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    prefix_blocks = prefix_len // bs
+    lengths = [prefix_len + h + q for h, q in plan]
+    own = [-(-L // bs) - prefix_blocks for L in lengths]
+    pool = rng.permutation(prefix_blocks + sum(own) + 5)
+    num_blocks = len(pool) + 1
+    shared = pool[:prefix_blocks].tolist()
+    tables, cursor = [], prefix_blocks
+    for n in own:
+        tables.append(shared + pool[cursor : cursor + n].tolist())
+        cursor += n
+    cache = torch.full((2, num_blocks, bs, hkv, d), float("nan"), dtype=torch.bfloat16, device=device)
+    flat = cache.view(2, -1, hkv, d)
+    pos = torch.arange(prefix_len, device=device)
+    slots = map_cache_slots(pos, torch.tensor(shared, device=device), bs)
+    flat[:, slots] = torch.randn((2, prefix_len, hkv, d), generator=gen, device=device).to(torch.bfloat16)
+    suffix = {}
+    for r, (h, q) in enumerate(plan):
+        if h:
+            hist = torch.arange(prefix_len, prefix_len + h, device=device)
+            rows = torch.randn((2, h, hkv, d), generator=gen, device=device).to(torch.bfloat16)
+            suffix[r] = rows
+            flat[:, map_cache_slots(hist, torch.tensor(tables[r], device=device), bs)] = rows
+    for first, second in twins:
+        if plan[second][0]:
+            hist = torch.arange(prefix_len, prefix_len + plan[second][0], device=device)
+            flat[:, map_cache_slots(hist, torch.tensor(tables[second], device=device), bs)] = suffix[first]
+    positions = [list(range(L - q, L)) for L, (_, q) in zip(lengths, plan)]
+    b = oracle.make_batch(positions, tables, block_size=bs, null_block_id=num_blocks - 1)
+    md = AttentionMetadata(
+        query_positions=torch.as_tensor(b.query_positions, device=device),
+        query_context_start_positions=torch.as_tensor(b.query_context_start_positions, device=device),
+        query_start_locations=torch.as_tensor(b.query_start_locations, device=device),
+        context_lengths=torch.as_tensor(b.context_lengths, device=device),
+        block_table=torch.as_tensor(b.block_table, device=device),
+        slot_mapping=torch.as_tensor(b.slot_mapping, device=device),
+        block_size=bs,
+        max_query_len=max(q for _, q in plan),
+    )
+    n = sum(q for _, q in plan)
+    q_, k_, v_ = (torch.randn((n, h_, d), generator=gen, device=device).to(torch.bfloat16) for h_ in (hq, hkv, hkv))
+    qsl = b.query_start_locations
+    for first, second in twins:
+        for t in (q_, k_, v_):
+            t[qsl[second] : qsl[second + 1]] = t[qsl[first] : qsl[first + 1]]
+    return q_, k_, v_, cache, md, shared
+
+
+def test_shared_prefix_requests_see_identical_history(device):
+    """The reference's shared-prefix case (test_reference.py:923-968) at
+    GPU scale: two requests share block 0 of a 16-token prefix and decode the
+    same token from different last blocks; both equal the dense oracle."""
+
+    q, k, v, cache, md, _ = shared_prefix_case(device, 16, [(0, 1), (0, 1)], 16, 8, seed=61, twins=[(0, 1)])
+    out = run_and_check(q, k, v, cache, md, torch.bfloat16)
+    assert torch.equal(out[0], out[1])
+
+
+@pytest.mark.parametrize(("hq", "hkv"), [(32, 8), (16, 8)], ids=["llama3", "qwen3"])
+def test_shared_4096_token_prefix_suffix_prefill_and_decode(device, hq, hkv):
+    """The Llama-3 e2e prefix-cache pattern: a 4,096-token prefix held once
+    (256 shared blocks) and read by every request; suffix prefill chunks
+    starting at the computed offset 4,096 and further in, beside decodes
+    whose suffixes run past it. The prefix blocks are never written; twin
+    requests (same suffix through different blocks) give identical rows."""
+
+    plan = [(0, 512), (0, 512), (1000, 300), (2500, 1), (37, 1), (0, 1), (4000, 64)]
+    q, k, v, cache, md, shared = shared_prefix_case(device, 4096, plan, hq, hkv, seed=62, twins=[(0, 1)])
+    prefix_before = cache[:, shared].clone()
+    out = run_and_check(q, k, v, cache, md, torch.bfloat16)
+    assert torch.equal(cache[:, shared].view(torch.int16), prefix_before.view(torch.int16))
+    assert torch.equal(out[:512], out[512:1024])
 
 
 def test_graph_replay_matches_eager(device):
