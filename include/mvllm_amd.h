@@ -187,6 +187,35 @@ int mvllm_attention_forward(const mvllm_tensor3* query,
                             int64_t workspace_bytes, void* stream);
 
 /*
+ * Device workspace held by mvllm_attention_forward_noalloc: 32 MiB per device.
+ * It covers the split-KV partials and work lists of batches such as 256
+ * decodes over a 512-block table with 32 query heads (about 21 MB).
+ */
+#define MVLLM_NOALLOC_SCRATCH_BYTES (32LL * 1024 * 1024)
+
+/*
+ * mvllm_attention_forward without a workspace argument: for callers that
+ * cannot allocate device memory (code under HIP graph capture that may not
+ * grow a pool, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The workspace is a library-owned device
+ * array of MVLLM_NOALLOC_SCRATCH_BYTES per device (its address is looked up
+ * once per device on the first call there); the call allocates nothing and
+ * runs all of its work on `stream` (no side stream). A batch that needs more
+ * workspace (mvllm_attention_workspace_bytes) is rejected with
+ * MVLLM_ERR_WORKSPACE. Every call on one device shares that array: calls
+ * that overlap on one device (other streams, other threads) race and give
+ * wrong results. The array needs no initialisation: every call writes what
+ * it reads.
+ */
+int mvllm_attention_forward_noalloc(const mvllm_tensor3* query,
+                                    const mvllm_tensor3* key,
+                                    const mvllm_tensor3* value,
+                                    const mvllm_kv_cache* cache,
+                                    const mvllm_batch* batch,
+                                    const mvllm_tensor3* out, float scale,
+                                    void* stream);
+
+/*
  * Optional kernel timing for measurement: hipEvent_t handles (as void*,
  * NULL = not wanted) recorded on the launch stream immediately before and
  * after the decode kernel and the prefill kernel (hipExtLaunchKernel).

@@ -245,7 +245,7 @@ int attention_plan(const mvllm_batch* batch, int64_t Hq, const mvllm_kv_cache* c
 int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
                     const mvllm_batch* batch, const mvllm_tensor3* out, float scale,
                     void* workspace, int64_t workspace_bytes, const mvllm_timing* timing,
-                    void* stream, bool planned = false) {
+                    void* stream, bool planned = false, bool single_stream = false) {
   if (int rc = check_tensor(query, "query")) return rc;
   if (int rc = check_tensor(out, "out")) return rc;
   if (!cache || !cache->data) return fail(MVLLM_ERR_INVALID, "cache is null");
@@ -294,7 +294,7 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
   if (batch->max_query_len != 1 && prefill_supported(a, dtype)) {
     // A fork and join cost ~10 us: the prefill moves to the side stream only
     // when the hint says that the batch holds multi-query requests.
-    SideStream* side = batch->max_query_len > 1 ? side_stream(s) : nullptr;
+    SideStream* side = batch->max_query_len > 1 && !single_stream ? side_stream(s) : nullptr;
     hipStream_t pst = s;
     if (side) {
       MVLLM_HIP_TRY(hipEventRecord(side->fork, s));
@@ -321,7 +321,7 @@ int attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,
                       const mvllm_tensor3* value, const mvllm_kv_cache* cache,
                       const mvllm_batch* batch, const mvllm_tensor3* out, float scale,
                       void* workspace, int64_t workspace_bytes, const mvllm_timing* timing,
-                      void* stream) {
+                      void* stream, bool single_stream = false) {
   if (!batch) return fail(MVLLM_ERR_INVALID, "batch is null");
   if (batch->num_tokens > 0) {
     if (!batch->slot_mapping) return fail(MVLLM_ERR_INVALID, "slot_mapping is null");
@@ -329,7 +329,52 @@ int attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,
       return rc;
   }
   return paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, timing,
-                         stream);
+                         stream, false, single_stream);
+}
+
+}  // namespace
+}  // namespace mvllm
+
+// ---- the allocation-free entry point ------------------------------------------
+//
+// mvllm_attention_forward_noalloc takes its workspace (split-KV partials and
+// work lists) from this file-scope device array instead of a caller
+// argument. Each device holds its own copy from the library's first use on
+// it until the process ends. In host code `scratch` names a host-side
+// stand-in, never the device memory: its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+static __device__ __align__(256) unsigned char scratch[MVLLM_NOALLOC_SCRATCH_BYTES];
+
+namespace mvllm {
+namespace {
+
+// Device address of `scratch` on the device that `stream` belongs to,
+// looked up on the first call for that device (with it current) and kept.
+int scratch_address(hipStream_t stream, void** out) {
+  static std::mutex mu;
+  static void* per_device[64] = {nullptr};
+  int dev = 0;
+  if (stream) {
+    MVLLM_HIP_TRY(hipStreamGetDevice(stream, &dev));
+  } else {
+    MVLLM_HIP_TRY(hipGetDevice(&dev));
+  }
+  if (dev < 0 || dev >= 64) return fail(MVLLM_ERR_INVALID, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!per_device[dev]) {
+    int current = 0;
+    MVLLM_HIP_TRY(hipGetDevice(&current));
+    if (current != dev) MVLLM_HIP_TRY(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (current != dev) MVLLM_HIP_TRY(hipSetDevice(current));
+    if (status != hipSuccess || !p)
+      return fail(MVLLM_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(status));
+    per_device[dev] = p;
+  }
+  *out = per_device[dev];
+  return MVLLM_OK;
 }
 
 }  // namespace
@@ -381,4 +426,27 @@ extern "C" int mvllm_attention_forward_timed(const mvllm_tensor3* query,
   clear_error();
   return attention_forward(query, key, value, cache, batch, out, scale, workspace,
                            workspace_bytes, timing, stream);
+}
+
+extern "C" int mvllm_attention_forward_noalloc(const mvllm_tensor3* query,
+                                               const mvllm_tensor3* key,
+                                               const mvllm_tensor3* value,
+                                               const mvllm_kv_cache* cache,
+                                               const mvllm_batch* batch,
+                                               const mvllm_tensor3* out, float scale,
+                                               void* stream) {
+  clear_error();
+  if (!query || !batch || !cache) return fail(MVLLM_ERR_INVALID, "query, batch or cache is null");
+  const int64_t need = mvllm_attention_workspace_bytes(batch, query->size[1], query->size[2]);
+  if (need > MVLLM_NOALLOC_SCRATCH_BYTES)
+    return fail(MVLLM_ERR_WORKSPACE,
+                "batch needs %lld bytes of workspace; mvllm_attention_forward_noalloc holds at most %lld "
+                "(use mvllm_attention_forward with a caller workspace)",
+                (long long)need, (long long)MVLLM_NOALLOC_SCRATCH_BYTES);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if (int rc = scratch_address(s, &ws)) return rc;
+  // Everything stays on the caller's stream: no side stream is created.
+  return attention_forward(query, key, value, cache, batch, out, scale, ws, MVLLM_NOALLOC_SCRATCH_BYTES,
+                           nullptr, stream, true);
 }

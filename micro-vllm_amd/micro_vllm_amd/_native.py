@@ -33,6 +33,9 @@ ERR_UNSUPPORTED = -2
 ERR_HIP = -3
 ERR_WORKSPACE = -4
 
+# Device workspace of mvllm_attention_forward_noalloc (MVLLM_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
+
 # Every function declared in include/mvllm_amd.h.
 EXPORTED_SYMBOLS = (
     "mvllm_kv_write",
@@ -42,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_paged_attention_planned",
     "mvllm_attention_forward",
     "mvllm_attention_forward_timed",
+    "mvllm_attention_forward_noalloc",
     "mvllm_gather_kv",
     "mvllm_context_starts",
     "mvllm_pack_batch",
@@ -172,6 +176,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_float, _ptr, _i64, p(Timing), _ptr,
     ]
     lib.mvllm_attention_forward_timed.restype = ctypes.c_int
+    lib.mvllm_attention_forward_noalloc.argtypes = [
+        p(Tensor3), p(Tensor3), p(Tensor3), p(KVCache), p(Batch), p(Tensor3), ctypes.c_float, _ptr,
+    ]
+    lib.mvllm_attention_forward_noalloc.restype = ctypes.c_int
     lib.mvllm_gather_kv.argtypes = [p(KVCache), p(Batch), _i64, _ptr, _ptr, _ptr]
     lib.mvllm_gather_kv.restype = ctypes.c_int
     lib.mvllm_context_starts.argtypes = [_ptr, _i64, ctypes.c_int32, _i64, _ptr, _ptr]

@@ -137,3 +137,21 @@ def test_map_cache_slots_matches_reference_vector():
     # tests/worker/test_model_runner.py:383-402: positions 3, 4 with blocks (2, 5), block 4.
     slots = map_cache_slots(torch.tensor([3, 4]), torch.tensor([2, 5]), 4)
     assert slots.tolist() == [11, 20]
+
+
+def test_noalloc_entry_point_rejects_batches_beyond_its_workspace():
+    """The allocation-free entry point checks the batch's workspace need
+    against its fixed device array before it touches any pointer."""
+
+    lib = _native.load()
+    q = _native.Tensor3()
+    q.dtype = _native.DTYPE_BF16
+    q.size[0], q.size[1], q.size[2] = 4096, 32, 128
+    b = _native.Batch()
+    b.num_tokens, b.num_requests, b.block_table_width, b.block_size = 4096, 4096, 2048, 16
+    need = lib.mvllm_attention_workspace_bytes(b, 32, 128)
+    assert need > _native.NOALLOC_SCRATCH_BYTES
+    status = lib.mvllm_attention_forward_noalloc(q, q, q, _native.KVCache(), b, q, 1.0, None)
+    assert status == _native.ERR_WORKSPACE
+    message = lib.mvllm_last_error()
+    assert str(need).encode() in message and str(_native.NOALLOC_SCRATCH_BYTES).encode() in message
