@@ -1,23 +1,32 @@
 """End-to-end greedy decoding with the HIP operator against the torch
 restatement of the reference operator.
 
-A random-init Qwen3-shaped decoder (2 layers, 16/8 heads of 128, qk-norm)
-generates with the `mi355x_paged` operator under a small token budget, so
-prompts are prefilled in chunks and decode steps mix with prefill chunks.
-Every generated position is then re-derived teacher-forced with the
-reference-semantics operator on the same weights: the greedy token must be
-the same, except where the reference's two largest logits are within bf16
-noise of each other (a legitimate near-tie; the survey's rule for
-random-init models), and the logits of both operators must agree to bf16
-accuracy.
+Random-init Qwen3- and Llama-shaped decoders generate with the
+`mi355x_paged` operator under token budgets that force chunked prefill and
+mixed steps. Every generated position is then re-derived teacher-forced with
+the reference-semantics operator (`tests/_torch_reference.py`) on the same
+weights, and the greedy tokens must be IDENTICAL, with no allowance.
+
+Identity of greedy tokens is only decidable where the reference's top-2
+logit gap exceeds the rounding noise between two correct bf16
+implementations. The token tests therefore use the copy-head init of
+`tests/_copy_model.py`: the attention of layer 0 picks the token at
+t - 37 with a gap of several logit units. Each test asserts that premise
+(the smallest gap is at least 4x the largest logit difference between the
+two operators on the same sequences), reports the first divergent position
+and its gap if there is one, and fails on it. Plain random-init models are
+checked through their logits (no token claim): `test_random_init_logits_*`.
 """
 
 from __future__ import annotations
+
+import copy
 
 import numpy as np
 import pytest
 import torch
 
+from _copy_model import make_copy_model
 from _torch_reference import TorchReferenceAttention
 from micro_vllm_amd.attention.operators.registry import get_attention_operator_class
 from micro_vllm_amd.attention.spec import FullAttentionSpec
@@ -28,17 +37,14 @@ from micro_vllm_amd.worker.scheduler_output import CacheGroupBlockTable, Schedul
 pytestmark = pytest.mark.gpu
 
 VOCAB = 8192
-# Logits have std ~0.64 at this init and are produced in bf16 (one ulp is
-# ~0.016 at magnitude 2), so a top-2 gap below ~3 ulps is a near-tie that a
-# one-ulp difference in an attention output can flip.
-NEAR_TIE = 0.05
-LOGIT_ATOL = 0.15     # max |logit difference| between the two operators
+COPY_OFFSET = 37
+GAP_OVER_NOISE = 4.0   # smallest reference top-2 gap / largest logit difference
 
 
-def make_requests(seed, count, lo, hi, max_tokens):
+def make_requests(seed, count, lo, hi, max_tokens, vocab=VOCAB):
     rng = np.random.default_rng(seed)
     return [
-        Request(f"r{i}", rng.integers(0, VOCAB, size=int(rng.integers(lo, hi + 1))).tolist(), max_tokens)
+        Request(f"r{i}", rng.integers(0, vocab, size=int(rng.integers(lo, hi + 1))).tolist(), max_tokens)
         for i in range(count)
     ]
 
@@ -63,21 +69,21 @@ def teacher_forced_logits(model, sequences, device):
         SchedulerOutput(tuple(plan_items)), specs=[FullAttentionSpec()], block_size=16, null_block_id=block, device=device
     )
     hidden = model.forward(packed.input_ids, packed.positions, caches, packed.group_metadata[0])
+    del caches
     return model.logits(hidden).float()
 
 
 def check_against_reference(requests, hip_model, ref_model, device):
-    """Teacher-forced check of every generated position (see module doc)."""
+    """Teacher-forced check of every generated position (see module doc):
+    identical greedy tokens, on a margin the test verifies."""
 
     sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in requests]
     ref_logits = teacher_forced_logits(ref_model, sequences, device)
     hip_logits = teacher_forced_logits(hip_model, sequences, device)
     assert torch.isfinite(hip_logits).all()
     max_diff = (hip_logits - ref_logits).abs().max().item()
-    print(f"max |logit difference| {max_diff:.4f}")
-    assert max_diff < LOGIT_ATOL
 
-    offset, checked, near_ties = 0, 0, 0
+    offset, checked, min_gap, divergence = 0, 0, float("inf"), None
     for r, seq in zip(requests, sequences):
         first = len(r.prompt_token_ids) - 1
         rows = ref_logits[offset + first : offset + len(seq)]
@@ -85,28 +91,40 @@ def check_against_reference(requests, hip_model, ref_model, device):
         top2 = rows.topk(2, dim=-1)
         expected = top2.indices[:, 0].tolist()
         gap = (top2.values[:, 0] - top2.values[:, 1]).tolist()
-        for got, want, g in zip(r.output_token_ids, expected, gap):
+        for i, (got, want, g) in enumerate(zip(r.output_token_ids, expected, gap)):
             checked += 1
-            if got != want:
-                near_ties += 1
-                assert g < NEAR_TIE, f"{r.request_id}: token {got} != {want} with a reference logit gap of {g:.4f}"
-    print(f"{checked} positions, {near_ties} near-tie flips")
-    assert near_ties <= checked // 10
+            min_gap = min(min_gap, g)
+            if got != want and divergence is None:
+                divergence = (r.request_id, i, got, want, g)
+    print(f"{checked} positions; max |logit difference| {max_diff:.4f}; smallest reference top-2 gap {min_gap:.3f}")
+    if divergence is not None:
+        print("first divergence: request %s output %d: got %d, reference %d (reference gap %.4f)" % divergence)
+    assert min_gap > GAP_OVER_NOISE * max_diff, "the init does not separate the top-2 logits beyond the noise"
+    assert divergence is None, "greedy tokens differ from the reference-semantics operator"
     return checked
 
 
-def models(device, seed=3, fused_layers=False, **overrides):
-    cfg = DecoderConfig.qwen3_0_6b(num_hidden_layers=2, vocab_size=VOCAB, **overrides)
+def models(device, seed=3, fused_layers=False, copy_head=True, **overrides):
+    """The HIP model and the reference-semantics model on the same weights."""
+
+    base = overrides.pop("base", DecoderConfig.qwen3_0_6b)
+    overrides.setdefault("num_hidden_layers", 2)
+    overrides.setdefault("vocab_size", VOCAB)
+    cfg = base(**overrides)
     hip_model = DecoderModel(
         cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed, fused_layers=fused_layers
     )
-    ref_model = DecoderModel(cfg, TorchReferenceAttention(), device=device, seed=seed)
+    if copy_head:
+        make_copy_model(hip_model, offset=COPY_OFFSET)
+    ref_model = copy.copy(hip_model)  # the same weight tensors
+    ref_model.operator = TorchReferenceAttention()
+    ref_model.fused_layers = False
     return hip_model, ref_model
 
 
 def test_greedy_decoding_matches_reference_attention(device):
     hip_model, ref_model = models(device)
-    requests = make_requests(seed=1, count=8, lo=20, hi=200, max_tokens=12)
+    requests = make_requests(seed=1, count=8, lo=40, hi=200, max_tokens=12)
     engine = GenerationEngine(hip_model, num_blocks=256, max_num_batched_tokens=160, max_num_seqs=6, max_model_len=512)
     result = engine.generate(requests)
     assert result.output_tokens == 8 * 12
@@ -116,7 +134,7 @@ def test_greedy_decoding_matches_reference_attention(device):
 
 def test_greedy_decoding_with_decode_graphs_matches_reference_attention(device):
     hip_model, ref_model = models(device, seed=5)
-    requests = make_requests(seed=2, count=7, lo=10, hi=150, max_tokens=16)
+    requests = make_requests(seed=2, count=7, lo=40, hi=150, max_tokens=16)
     engine = GenerationEngine(
         hip_model, num_blocks=256, max_num_batched_tokens=512, max_num_seqs=8, max_model_len=512, decode_graphs=True
     )
@@ -133,7 +151,7 @@ def test_fused_layer_kernels_match_reference_decoding(device, qk_norm):
     reference-semantics operator."""
 
     hip_model, ref_model = models(device, seed=9, fused_layers=True, qk_norm=qk_norm)
-    requests = make_requests(seed=6, count=7, lo=10, hi=160, max_tokens=12)
+    requests = make_requests(seed=6, count=7, lo=40, hi=160, max_tokens=12)
     engine = GenerationEngine(
         hip_model, num_blocks=256, max_num_batched_tokens=200, max_num_seqs=8, max_model_len=512, decode_graphs=True
     )
@@ -225,3 +243,60 @@ def test_decode_graph_replays_match_eager_on_the_same_buffers(device):
             assert torch.equal(entry.logits, eager_logits)
             assert torch.equal(entry.tokens, eager_tokens)
             _ = (eager_logits.float() * 2).sum().item()  # eager work between replays
+
+
+QWEN3_VOCAB = 151_936
+
+
+def test_qwen3_0_6b_shape_greedy_tokens_match_reference(device):
+    """The end-to-end Qwen3-0.6B configuration's model at its real shape (28
+    layers, hidden 1024, 16/8 heads of 128, qk-norm, MLP 3072, vocab
+    151,936, tied embeddings) through the bench's engine path: fused layer
+    kernels, chunked prefill under a 2,048-token budget, HIP-graph decode
+    steps, host one step ahead. 12 requests with prompts U[64, 1024] and 32
+    greedy tokens each; every token must equal the reference-semantics
+    operator's teacher-forced greedy choice (tests/integration/
+    test_real_model_engine.py:183-207 asks the same of the real model)."""
+
+    hip_model, ref_model = models(device, seed=21, fused_layers=True, num_hidden_layers=28, vocab_size=QWEN3_VOCAB)
+    requests = make_requests(seed=21, count=12, lo=64, hi=1024, max_tokens=32, vocab=QWEN3_VOCAB)
+    engine = GenerationEngine(
+        hip_model,
+        num_blocks=2048,
+        max_num_batched_tokens=2048,
+        max_num_seqs=8,
+        max_model_len=1100,
+        decode_graphs=True,
+        pipeline=True,
+    )
+    result = engine.generate(requests)
+    assert result.output_tokens == 12 * 32
+    assert check_against_reference(requests, hip_model, ref_model, device) == 12 * 32
+
+
+def test_random_init_logits_agree_at_qwen3_0_6b_shape(device):
+    """Plain random init (no copy head) at the real Qwen3-0.6B shape: the
+    teacher-forced logits of the HIP path (fused layer kernels, HIP
+    attention) and of the reference-semantics path (torch layers, torch
+    reference attention) on six sequences of U[64, 1024] tokens. Logits have
+    a standard deviation of ~0.6 here; bf16 rounding of the two paths may
+    differ by a few units in the last place of a logit (0.0039-0.0156 at
+    these magnitudes), so the bound is 0.25 on the largest difference and
+    0.01 on the mean."""
+
+    hip_model, ref_model = models(
+        device, seed=22, fused_layers=True, copy_head=False, num_hidden_layers=28, vocab_size=QWEN3_VOCAB
+    )
+    rng = np.random.default_rng(22)
+    sequences = [rng.integers(0, QWEN3_VOCAB, size=int(rng.integers(64, 1025))).tolist() for _ in range(6)]
+    ref = teacher_forced_logits(ref_model, sequences, device)
+    hip = teacher_forced_logits(hip_model, sequences, device)
+    diff = (hip - ref).abs()
+    flips = (hip.argmax(-1) != ref.argmax(-1)).sum().item()
+    print(
+        f"logit std {ref.std().item():.3f}; max |diff| {diff.max().item():.4f}; mean {diff.mean().item():.5f}; "
+        f"greedy flips {flips} of {ref.shape[0]} positions (no token claim at this init)"
+    )
+    assert torch.isfinite(hip).all()
+    assert diff.max().item() < 0.25
+    assert diff.mean().item() < 0.01
