@@ -1,4 +1,4 @@
-"""Benchmark of the ragged paged-attention step on one MI355X.
+"""Benchmark of the ragged paged-attention path on one MI355X.
 
 A step is one pass of the hot path over one synthetic batch: the
 ``mi355x_paged`` operator's forward (KV-cache write + split-KV decode +
@@ -11,17 +11,25 @@ Reported (one JSON line on stdout):
 * ``value``: algorithmic HBM bytes of the step / step time, in GB/s;
 * ``roofline``: the decode kernel's algorithmic bytes per launch / its mean
   duration measured with HIP events recorded around its launch, against
-  the 8 TB/s HBM peak (``llama3_mixed``: the step runs the prefill kernel
-  beside the decode kernel on a second stream; ``value`` is that step, and
-  the two kernels' rooflines come from a second pass with the overlap
-  switched off, reported under ``overlap``);
+  the 8 TB/s HBM peak;
+* ``prefill``: the prefill kernel on the Llama-3-head mixed batch (8 chunks
+  of 512 + 248 decodes): causal-visible FLOPs / its mean duration, against
+  the 2.5 PFLOP/s bf16 peak (serial pass), and the mixed step's time with
+  the prefill beside the decode kernel;
+* ``e2e``: Qwen3-0.6B-shaped end-to-end output tok/s, synchronized steps
+  summed (the reference's method) and, as ``value_pipelined``, with the host
+  one graph step ahead;
 * ``gpu_baseline``: the same step in plain torch (block-table gather and
   matmuls) timed on the same GPU, and the HIP path's speedup over it;
-* ``cpu_baseline``: the numpy oracle (a restatement of the reference's
-  CPU attention) timed on this host, single-threaded, on a sample of the
-  same batch.
+* ``cpu_baseline``: the reference operator's CPU path (torch, bf16 cache,
+  fp32 math, every available host core) on the same batch.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload qwen3_decode]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload qwen3_decode] [--quick]
+
+Other workloads: ``llama3_mixed``, ``llama3_long_decode`` (attention steps),
+``qwen3_e2e`` and ``llama3_e2e`` (end-to-end generation; the Llama-3-8B one
+shares a 4,096-token prefix through the prefix cache and holds a ~200 GB KV
+cache).
 """
 
 from __future__ import annotations
@@ -121,66 +129,98 @@ def measured_traffic(workload: str) -> int | None:
     return None
 
 
-def cpu_baseline(w, sample_requests: int, repeats: int) -> dict:
-    """Time the numpy oracle, single-threaded, on ``sample_requests``
-    sequences of the batch (their blocks copied into a compact host cache)."""
+def host_threads() -> int:
+    """Host threads for the CPU baseline: every core this process may use,
+    capped by OMP_NUM_THREADS when it is set (the GPU box's CPU share)."""
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        cores = min(cores, int(env))
+    return max(1, cores)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(w, sample_requests: int, repeats: int, warmups: int = 2) -> dict:
+    """Time the reference operator's CPU path (``oracle.reference_cpu``: the
+    steps of reference.py:14-138 in torch, bf16 cache, fp32 math) on this
+    host's cores, on ``sample_requests`` sequences of the batch (their blocks
+    copied into a compact host cache, the step's own K/V written by the
+    forward). Median of ``repeats`` runs after ``warmups``."""
 
     import numpy as np
     import torch
 
-    import oracle
+    from oracle import reference_cpu
 
+    threads = host_threads()
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
     try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    order = np.arange(len(w.context_lengths))
-    step = max(1, len(order) // sample_requests)
-    chosen = order[::step][:sample_requests]
-    blocks = [w.block_lists[r] for r in chosen]
-    ids = np.concatenate(blocks)
-    compact = w.cache[:, torch.as_tensor(ids, device=w.cache.device)].cpu()
-    as_bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
-    cache = as_bits(compact)
-    cache = np.concatenate([cache, np.zeros_like(cache[:, :1])], axis=1)
-    tables, positions, cursor = [], [], 0
-    for r, b in zip(chosen, blocks):
-        tables.append(list(range(cursor, cursor + len(b))))
-        cursor += len(b)
-        L, q = int(w.context_lengths[r]), int(w.query_lengths[r])
-        positions.append(list(range(L - q, L)))
-    batch = oracle.make_batch(positions, tables, block_size=w.block_size, null_block_id=len(ids))
-    qsl = w.metadata.query_start_locations.cpu().numpy()
-    rows = np.concatenate([np.arange(qsl[r], qsl[r + 1]) for r in chosen])
-    rows_t = torch.as_tensor(rows, device=w.query.device)
-    q = as_bits(w.query[rows_t].cpu())
-    k = as_bits(w.key[rows_t].cpu())
-    v = as_bits(w.value[rows_t].cpu())
+        order = np.arange(len(w.context_lengths))
+        step = max(1, len(order) // sample_requests)
+        chosen = order[::step][:sample_requests]
+        blocks = [w.block_lists[r] for r in chosen]
+        ids = np.concatenate(blocks)
+        compact = w.cache[:, torch.as_tensor(ids, device=w.cache.device)].cpu()
+        cache = torch.cat([compact, torch.zeros_like(compact[:, :1])], dim=1)
+        null = len(ids)
+        width = max(len(b) for b in blocks)
+        table = torch.full((len(chosen), width), null, dtype=torch.int64)
+        cursor = 0
+        positions, qsl, lengths = [], [0], []
+        for i, (r, b) in enumerate(zip(chosen, blocks)):
+            table[i, : len(b)] = torch.arange(cursor, cursor + len(b))
+            cursor += len(b)
+            L, q = int(w.context_lengths[r]), int(w.query_lengths[r])
+            positions.extend(range(L - q, L))
+            qsl.append(qsl[-1] + q)
+            lengths.append(L)
+        pos = torch.tensor(positions, dtype=torch.int64)
+        starts = torch.zeros_like(pos)
+        req = torch.repeat_interleave(torch.arange(len(chosen)), torch.tensor(np.diff(qsl)))
+        slots = table[req, pos // w.block_size] * w.block_size + pos % w.block_size
+        full_qsl = w.metadata.query_start_locations.cpu().numpy()
+        rows = np.concatenate([np.arange(full_qsl[r], full_qsl[r + 1]) for r in chosen])
+        rows_t = torch.as_tensor(rows, device=w.query.device)
+        q, k, v = (t[rows_t].cpu() for t in (w.query, w.key, w.value))
+        qsl_t, len_t = torch.tensor(qsl, dtype=torch.int64), torch.tensor(lengths, dtype=torch.int64)
 
-    def run():
-        work = cache.copy()
-        start = time.perf_counter()
-        oracle.reference_forward(q, k, v, work, batch)
-        return time.perf_counter() - start
+        def run():
+            start = time.perf_counter()
+            reference_cpu.reference_forward(q, k, v, cache, pos, starts, qsl_t, len_t, table, slots, w.block_size)
+            return time.perf_counter() - start
 
-    limiter = threadpool_limits(limits=1) if threadpool_limits else None
-    try:
-        run()
+        for _ in range(warmups):
+            run()
         times = [run() for _ in range(repeats)]
     finally:
-        if limiter is not None:
-            limiter.unregister()
+        torch.set_num_threads(previous)
     seconds = statistics.median(times)
     sample_bytes = _subset_bytes(w, chosen)
     return {
         "value": round(sample_bytes / seconds / 1e9, 4),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model(),
         "sample": (
             f"{len(chosen)} of {len(w.context_lengths)} sequences "
-            f"({int(w.context_lengths[chosen].sum())} context tokens), numpy oracle single-threaded, "
-            f"median of {repeats} runs: {seconds:.3f} s"
+            f"({int(w.context_lengths[chosen].sum())} context tokens) through the reference operator's CPU path "
+            f"(torch, {threads} threads, bf16 cache, fp32 math), median of {repeats} runs after {warmups}: "
+            f"{seconds:.3f} s per forward"
         ),
     }
 
@@ -296,9 +336,27 @@ def _subset_bytes(w, chosen) -> int:
     return int(L.sum()) * w.num_kv_heads * w.head_dim * 2 * es + 2 * n * w.num_q_heads * w.head_dim * es
 
 
-def run_e2e(args, device) -> dict:
-    """Greedy generation with a random-init Qwen3-0.6B-shaped model: output
-    tokens per second of synchronized engine steps."""
+E2E_CONFIGS = {
+    # The Qwen3-0.6B end-to-end configuration: 256 random prompts U[64, 1024],
+    # 256 greedy tokens each, 8,192-token budget, up to 256 sequences.
+    "qwen3_e2e": dict(model="qwen3_0_6b", requests=256, prompt=(64, 1024), prefix=0, max_tokens=256,
+                      max_num_seqs=256, prefix_cache=False, kv_bytes=None),
+    # The Llama-3-8B end-to-end configuration: 64 requests sharing a
+    # 4,096-token random prefix, each with its own suffix U[4096, 28672],
+    # 512 greedy tokens each, KV cache of ~200 GB, prefix cache on.
+    "llama3_e2e": dict(model="llama3_8b", requests=64, prompt=(4096, 28672), prefix=4096, max_tokens=512,
+                       max_num_seqs=64, prefix_cache=True, kv_bytes=200e9),
+}
+
+
+def run_generation(device, workload: str, *, modes=("sync",), requests: int | None = None,
+                   max_tokens: int | None = None, unfused: bool = False, seed: int = 0) -> dict:
+    """Greedy generation with a random-init decoder through the harness
+    engine. ``modes``: "sync" times synchronized steps and sums them (the
+    reference's method, benchmarks/benchmark_engine.py:305-315: each step is
+    schedule + execute + synchronize + update); "pipelined" lets the host run
+    one graph step ahead and times the loop's wall clock; "eager" runs sync
+    without HIP graphs. Returns one record per mode."""
 
     import numpy as np
     import torch
@@ -306,71 +364,63 @@ def run_e2e(args, device) -> dict:
     from micro_vllm_amd.attention.operators.registry import get_attention_operator_class
     from micro_vllm_amd.harness import DecoderConfig, DecoderModel, GenerationEngine, Request
 
-    cfg = DecoderConfig.qwen3_0_6b()
-    model = DecoderModel(
-        cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=0, fused_layers=not args.e2e_unfused
-    )
-    rng = np.random.default_rng(0)
-    lengths = rng.integers(64, 1025, size=args.e2e_requests)
-    prompts = [rng.integers(0, cfg.vocab_size, size=int(n)).tolist() for n in lengths]
+    spec = dict(E2E_CONFIGS[workload])
+    if requests is not None:
+        spec["requests"] = requests
+    if max_tokens is not None:
+        spec["max_tokens"] = max_tokens
+    cfg = getattr(DecoderConfig, spec["model"])()
+    model = DecoderModel(cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed,
+                         fused_layers=not unfused)
+    rng = np.random.default_rng(seed)
+    lo, hi = spec["prompt"]
+    lengths = rng.integers(lo, hi + 1, size=spec["requests"])
+    prefix = rng.integers(0, cfg.vocab_size, size=spec["prefix"]).tolist()
+    prompts = [prefix + rng.integers(0, cfg.vocab_size, size=int(n)).tolist() for n in lengths]
     block_size = 16
-    per_request = -(-(int(lengths.max()) + args.e2e_max_tokens) // block_size)
-    num_blocks = per_request * args.e2e_requests + 1
+    longest = spec["prefix"] + int(lengths.max()) + spec["max_tokens"]
+    per_request = -(-longest // block_size)
+    if spec["kv_bytes"] is not None:
+        block_bytes = cfg.num_hidden_layers * 2 * block_size * cfg.num_key_value_heads * cfg.head_dim * 2
+        num_blocks = int(spec["kv_bytes"] // block_bytes)
+    else:
+        num_blocks = per_request * spec["requests"] + 1
+    max_model_len = per_request * block_size
 
-    # Warm-up: a few short requests through a separate engine (kernel loading, allocator).
+    # Warm-up: a few short requests through a small engine (kernel loading, allocator).
     warm = GenerationEngine(model, num_blocks=4 * 8 + 1, max_num_batched_tokens=8192, max_num_seqs=256)
     warm.generate([Request(f"w{i}", prompts[i][:64], max_tokens=4) for i in range(min(4, len(prompts)))])
     del warm
     torch.cuda.synchronize(device)
 
-    max_model_len = per_request * block_size
-    engine = GenerationEngine(
-        model,
-        num_blocks=num_blocks,
-        max_num_batched_tokens=8192,
-        max_num_seqs=256,
-        max_model_len=max_model_len,
-        decode_graphs=not args.e2e_eager,
-        pipeline=not args.e2e_eager and not args.e2e_sync,
-    )
-    if engine.graphs is not None:
-        # Capture every bucket before timing (the reference captures at start-up, model_runner.py:344-497).
-        for size in engine.graphs.BUCKETS:
-            if size <= 256:
-                engine.graphs.capture(size)
-    requests = [Request(f"r{i}", p, max_tokens=args.e2e_max_tokens) for i, p in enumerate(prompts)]
-    result = engine.generate(requests)
-    return {
-        "metric": METRIC,
-        "value": round(result.output_tokens_per_second, 2),
-        "unit": "output tok/s",
-        "n_gpus": 1,
-        "steps": result.steps,
-        "warmup": 1,
-        "ms_per_step": round(result.step_seconds / result.steps * 1e3, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": (
-                f"qwen3_e2e: Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads of 128, qk-norm, "
-                f"MLP 3072, vocab 151936, tied embeddings), random init seed 0, bf16; {args.e2e_requests} "
-                f"requests with random prompts U[64,1024], {args.e2e_max_tokens} greedy tokens each, "
-                "max_num_batched_tokens 8192, max_num_seqs 256, block 16, "
-                + ("eager" if args.e2e_eager else "decode steps as HIP graphs (buckets 1..256)")
-                + ("" if args.e2e_eager or args.e2e_sync else ", host one step ahead (pipelined)")
-                + ("; torch layers" if args.e2e_unfused else "; fused HIP layer kernels")
-            ),
-            "parameters": model.parameter_count(),
-            "prompt_tokens": result.prompt_tokens,
-            "output_tokens": result.output_tokens,
+    records = {}
+    for mode in modes:
+        engine = GenerationEngine(
+            model,
+            num_blocks=num_blocks,
+            max_num_batched_tokens=8192,
+            max_num_seqs=spec["max_num_seqs"],
+            max_model_len=max_model_len,
+            decode_graphs=mode != "eager",
+            pipeline=mode == "pipelined",
+            enable_prefix_cache=spec["prefix_cache"],
+            cache_namespace=spec["model"],
+        )
+        if engine.graphs is not None:
+            # Capture every bucket before timing (the reference captures at
+            # start-up, model_runner.py:344-497).
+            for size in engine.graphs.BUCKETS:
+                if size <= spec["max_num_seqs"]:
+                    engine.graphs.capture(size)
+        result = engine.generate([Request(f"r{i}", p, max_tokens=spec["max_tokens"]) for i, p in enumerate(prompts)])
+        records[mode] = {
+            "output_tok_s": round(result.output_tokens_per_second, 2),
+            "steps": result.steps,
             "step_seconds": round(result.step_seconds, 4),
             "timing": (
-                "synchronized steps summed"
-                if args.e2e_eager or args.e2e_sync
-                else "wall time of the generation loop (steps overlap)"
+                "wall time of the generation loop (steps overlap)"
+                if mode == "pipelined"
+                else "synchronized steps summed"
             ),
             "decode_steps": result.decode_steps,
             "decode_step_ms": round(result.decode_seconds / max(result.decode_steps, 1) * 1e3, 3),
@@ -379,8 +429,156 @@ def run_e2e(args, device) -> dict:
                 (result.step_seconds - result.decode_seconds) / max(result.steps - result.decode_steps, 1) * 1e3, 3
             ),
             "preemptions": result.preemptions,
-            "parallelism": "single GPU",
-        },
+            "prefix_hit_tokens": result.prefix_hit_tokens,
+            "output_tokens": result.output_tokens,
+            "prompt_tokens": result.prompt_tokens,
+        }
+        del engine
+        torch.cuda.synchronize(device)
+        torch.cuda.empty_cache()
+    c = cfg
+    description = (
+        f"{workload}: {spec['model']}-shaped decoder ({c.num_hidden_layers} layers, hidden {c.hidden_size}, "
+        f"{c.num_attention_heads}/{c.num_key_value_heads} heads of {c.head_dim}, MLP {c.intermediate_size}, "
+        f"vocab {c.vocab_size}{', qk-norm' if c.qk_norm else ''}), random init seed {seed}, bf16; "
+        f"{spec['requests']} requests with random prompts "
+        + (f"of a shared {spec['prefix']}-token prefix + " if spec["prefix"] else "")
+        + f"U[{lo},{hi}] tokens, {spec['max_tokens']} greedy tokens each, max_num_batched_tokens 8192, "
+        f"max_num_seqs {spec['max_num_seqs']}, block 16, {num_blocks} KV blocks"
+        + (", prefix cache on" if spec["prefix_cache"] else "")
+        + ("; torch layers" if unfused else "; fused HIP layer kernels")
+    )
+    return {"workload": description, "parameters": model.parameter_count(), "modes": records}
+
+
+def attention_workload(name: str, device):
+    from micro_vllm_amd import workloads
+
+    if name == "qwen3_decode":
+        return workloads.qwen3_decode(device), (
+            "qwen3_decode: 256 decode sequences, contexts U[128,4096] seed 0, 16 q / 8 kv heads, "
+            "head_dim 128, block 16, bf16, 70k-block shuffled pool, values N(0,1)*0.5"
+        )
+    if name == "llama3_long_decode":
+        return workloads.llama3_long_decode(device), (
+            "llama3_long_decode: 64 decode sequences, contexts U[8192,33280] seed 0, 32 q / 8 kv heads, "
+            "head_dim 128, block 16, bf16, values N(0,1)"
+        )
+    return workloads.llama3_mixed(device), (
+        "llama3_mixed: 8 prefill chunks x 512 at offsets U[0,2048] + 248 decodes U[256,8192], "
+        "32 q / 8 kv heads, head_dim 128, block 16, bf16"
+    )
+
+
+def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurrent: bool = True) -> dict:
+    """``warmup`` untimed forwards, then ``steps`` timed ones between HIP
+    events on the launch stream; per-kernel durations from the events the
+    library records around the decode and prefill launches. ``concurrent``
+    False keeps the prefill kernel on the caller's stream."""
+
+    import torch
+
+    from micro_vllm_amd import _native
+    from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
+
+    marks = hip.create(2)
+    decode_events = hip.create(2 * steps)
+    prefill_events = hip.create(2 * steps)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    previous = os.environ.get("MVLLM_PREFILL_CONCURRENT")
+    if not concurrent:
+        os.environ["MVLLM_PREFILL_CONCURRENT"] = "0"
+
+    def step(i: int | None):
+        timing = None
+        if i is not None:
+            timing = _native.Timing()
+            timing.decode_start, timing.decode_stop = decode_events[2 * i], decode_events[2 * i + 1]
+            timing.prefill_start, timing.prefill_stop = prefill_events[2 * i], prefill_events[2 * i + 1]
+        return hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata, timing=timing)
+
+    try:
+        for _ in range(warmup):
+            step(None)
+        torch.cuda.synchronize()
+        hip.hip.hipEventRecord(ctypes.c_void_p(marks[0]), ctypes.c_void_p(stream))
+        for i in range(steps):
+            step(i)
+        hip.hip.hipEventRecord(ctypes.c_void_p(marks[1]), ctypes.c_void_p(stream))
+        torch.cuda.synchronize()
+        out = {
+            "ms_per_step": hip.elapsed_ms(marks[0], marks[1]) / steps,
+            "decode_ms": statistics.mean(hip.elapsed_ms(decode_events[2 * i], decode_events[2 * i + 1]) for i in range(steps)),
+        }
+        out["prefill_ms"] = None
+        if (w.metadata.max_query_len or 0) > 1:
+            try:
+                out["prefill_ms"] = statistics.mean(
+                    hip.elapsed_ms(prefill_events[2 * i], prefill_events[2 * i + 1]) for i in range(steps)
+                )
+            except RuntimeError:
+                # No prefill launch was recorded (the generic kernel ran); the
+                # failed query leaves a HIP error behind: clear it.
+                hip.hip.hipGetLastError()
+    finally:
+        if not concurrent:
+            if previous is None:
+                del os.environ["MVLLM_PREFILL_CONCURRENT"]
+            else:
+                os.environ["MVLLM_PREFILL_CONCURRENT"] = previous
+        hip.destroy(marks + decode_events + prefill_events)
+    return out
+
+
+def prefill_record(w, timing: dict) -> dict:
+    from micro_vllm_amd import workloads
+
+    flops = workloads.prefill_flops(w)
+    if timing.get("prefill_ms") is None:
+        return {"flops": int(flops), "kernel_us": None, "note": "prefill ran on the generic kernel"}
+    tflops = flops / (timing["prefill_ms"] * 1e-3) / 1e12
+    return {
+        "kernel": "prefill_kernel<bf16>",
+        "bound": "mfma",
+        "flops": int(flops),
+        "kernel_us": round(timing["prefill_ms"] * 1e3, 2),
+        "achieved": round(tflops, 2),
+        "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+    }
+
+
+def e2e_line(args, device) -> dict:
+    """One JSON line for an end-to-end workload: the value is output tok/s of
+    the first timing mode (synchronized steps summed unless asked)."""
+
+    if args.e2e_eager:
+        modes = ("eager",)
+    elif args.e2e_pipelined:
+        modes = ("pipelined",)
+    else:
+        modes = ("sync",)
+    run = run_generation(
+        device, args.workload, modes=modes, requests=args.e2e_requests, max_tokens=args.e2e_max_tokens,
+        unfused=args.e2e_unfused,
+    )
+    rec = run["modes"][modes[0]]
+    return {
+        "metric": METRIC,
+        "value": rec["output_tok_s"],
+        "unit": "output tok/s",
+        "n_gpus": 1,
+        "steps": rec["steps"],
+        "warmup": 1,
+        "ms_per_step": round(rec["step_seconds"] / rec["steps"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": run["workload"], "parameters": run["parameters"], **rec, "parallelism": "single GPU"},
         "roofline": None,
         "cpu_baseline": None,
     }
@@ -392,21 +590,28 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument(
-        "--workload", default="qwen3_decode", choices=["qwen3_decode", "llama3_mixed", "llama3_long_decode", "qwen3_e2e"]
-    )
-    parser.add_argument("--e2e-requests", type=int, default=256, help="requests of the qwen3_e2e workload")
-    parser.add_argument("--e2e-max-tokens", type=int, default=256, help="greedy output tokens per request (qwen3_e2e)")
-    parser.add_argument("--e2e-eager", action="store_true", help="run qwen3_e2e decode steps eagerly (no HIP graphs)")
-    parser.add_argument(
-        "--e2e-unfused", action="store_true", help="qwen3_e2e with the torch layers instead of the fused HIP layer kernels"
+        "--workload",
+        default="qwen3_decode",
+        choices=["qwen3_decode", "llama3_mixed", "llama3_long_decode", "qwen3_e2e", "llama3_e2e"],
     )
     parser.add_argument(
-        "--e2e-sync",
+        "--quick",
         action="store_true",
-        help="qwen3_e2e graph steps one at a time (no host/GPU overlap), each step timed synchronized",
+        help="qwen3_decode without the mixed-batch prefill roofline and the Qwen3-0.6B end-to-end run",
+    )
+    parser.add_argument("--e2e-requests", type=int, default=None, help="requests of an end-to-end workload")
+    parser.add_argument("--e2e-max-tokens", type=int, default=None, help="greedy output tokens per request")
+    parser.add_argument("--e2e-eager", action="store_true", help="end-to-end steps eagerly (no HIP graphs)")
+    parser.add_argument(
+        "--e2e-unfused", action="store_true", help="end-to-end with the torch layers instead of the fused HIP layer kernels"
+    )
+    parser.add_argument(
+        "--e2e-pipelined",
+        action="store_true",
+        help="end-to-end with the host one graph step ahead (the loop's wall time instead of summed steps)",
     )
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
-    parser.add_argument("--cpu-repeats", type=int, default=10)
+    parser.add_argument("--cpu-repeats", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument(
         "--no-torch-baseline", action="store_true", help="skip the same-box torch gathered-attention baseline"
@@ -431,83 +636,31 @@ def main() -> int:
     import torch
 
     from micro_vllm_amd import _native, workloads
-    from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
 
     if not torch.cuda.is_available():
         print("bench.py needs a visible GPU", file=sys.stderr)
         return 1
     _native.load()
     device = torch.device("cuda", 0)
-    if args.workload == "qwen3_e2e":
-        print(json.dumps(run_e2e(args, device)), flush=True)
+    if args.workload in E2E_CONFIGS:
+        print(json.dumps(e2e_line(args, device)), flush=True)
         return 0
-    if args.workload == "qwen3_decode":
-        w = workloads.qwen3_decode(device)
-        description = (
-            "qwen3_decode: 256 decode sequences, contexts U[128,4096] seed 0, 16 q / 8 kv heads, "
-            "head_dim 128, block 16, bf16, 70k-block shuffled pool, values N(0,1)*0.5"
-        )
-    elif args.workload == "llama3_long_decode":
-        w = workloads.llama3_long_decode(device)
-        description = (
-            "llama3_long_decode: 64 decode sequences, contexts U[8192,33280] seed 0, 32 q / 8 kv heads, "
-            "head_dim 128, block 16, bf16, values N(0,1)"
-        )
-    else:
-        w = workloads.llama3_mixed(device)
-        description = (
-            "llama3_mixed: 8 prefill chunks x 512 at offsets U[0,2048] + 248 decodes U[256,8192], "
-            "32 q / 8 kv heads, head_dim 128, block 16, bf16"
-        )
+
+    w, description = attention_workload(args.workload, device)
     torch.cuda.synchronize()
-
     hip = HipEvents()
-    steps = args.steps
-    marks = hip.create(2)
-    decode_events = hip.create(2 * steps)
-    prefill_events = hip.create(2 * steps)
-    stream = torch.cuda.current_stream(device).cuda_stream
-    hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-
-    def step(i: int | None):
-        timing = None
-        if i is not None:
-            timing = _native.Timing()
-            timing.decode_start, timing.decode_stop = decode_events[2 * i], decode_events[2 * i + 1]
-            timing.prefill_start, timing.prefill_stop = prefill_events[2 * i], prefill_events[2 * i + 1]
-        return hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata, timing=timing)
-
-    def timed_pass() -> tuple[float, float]:
-        for _ in range(args.warmup):
-            step(None)
-        torch.cuda.synchronize()
-        hip.hip.hipEventRecord(ctypes.c_void_p(marks[0]), ctypes.c_void_p(stream))
-        for i in range(steps):
-            step(i)
-        hip.hip.hipEventRecord(ctypes.c_void_p(marks[1]), ctypes.c_void_p(stream))
-        torch.cuda.synchronize()
-        per_step = hip.elapsed_ms(marks[0], marks[1]) / steps
-        kernel = statistics.mean(hip.elapsed_ms(decode_events[2 * i], decode_events[2 * i + 1]) for i in range(steps))
-        return per_step, kernel
-
-    ms_per_step, decode_ms = timed_pass()
+    timing = time_attention(w, hip, device, args.steps, args.warmup)
+    ms_per_step, decode_ms = timing["ms_per_step"], timing["decode_ms"]
     overlap = None
     if args.workload == "llama3_mixed":
         # The library runs a mixed batch's prefill kernel on a second stream
         # beside the decode kernel, so their HIP-event spans overlap. The
         # step above is the shipped (overlapped) one; each kernel's roofline
         # comes from a second pass with the overlap switched off.
-        previous = os.environ.get("MVLLM_PREFILL_CONCURRENT")
-        os.environ["MVLLM_PREFILL_CONCURRENT"] = "0"
-        try:
-            serial_ms_per_step, decode_ms = timed_pass()
-        finally:
-            if previous is None:
-                del os.environ["MVLLM_PREFILL_CONCURRENT"]
-            else:
-                os.environ["MVLLM_PREFILL_CONCURRENT"] = previous
+        serial = time_attention(w, hip, device, args.steps, args.warmup, concurrent=False)
+        decode_ms = serial["decode_ms"]
         overlap = {
-            "ms_per_step_serial": round(serial_ms_per_step, 5),
+            "ms_per_step_serial": round(serial["ms_per_step"], 5),
             "note": "prefill on a second stream beside the decode kernel; kernel rooflines from the serial pass",
         }
 
@@ -520,7 +673,7 @@ def main() -> int:
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
@@ -558,18 +711,7 @@ def main() -> int:
     if overlap is not None:
         result["overlap"] = overlap
     if args.workload == "llama3_mixed":
-        flops = workloads.prefill_flops(w)
-        try:
-            prefill_ms = statistics.mean(hip.elapsed_ms(prefill_events[2 * i], prefill_events[2 * i + 1]) for i in range(steps))
-            result["prefill"] = {
-                "flops": int(flops),
-                "kernel_us": round(prefill_ms * 1e3, 2),
-                "achieved_tflops": round(flops / (prefill_ms * 1e-3) / 1e12, 2),
-                "peak_tflops": BF16_PEAK_TFLOPS,
-            }
-        except RuntimeError:
-            result["prefill"] = {"flops": int(flops), "kernel_us": None, "note": "prefill ran on the generic kernel"}
-    hip.destroy(marks + decode_events + prefill_events)
+        result["prefill"] = prefill_record(w, serial)
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=device)
@@ -579,16 +721,44 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     if not args.no_torch_baseline:
-        hip_out = step(None)
+        from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
+
+        hip_out = hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata)
         torch.cuda.synchronize()
         result["gpu_baseline"] = torch_baseline(w, hip_out)
         result["gpu_baseline"]["hip_speedup"] = round(result["gpu_baseline"]["ms_per_step"] / ms_per_step, 2)
         del hip_out
         torch.cuda.empty_cache()
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_sample, args.cpu_repeats)
-    else:
-        result["cpu_baseline"] = None
+    result["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline(w, args.cpu_sample, args.cpu_repeats)
+
+    if args.workload == "qwen3_decode" and not args.quick:
+        # The other targets on their own configurations, in the same line:
+        # the prefill kernel on the Llama-3 mixed batch (bf16 MFMA roofline)
+        # and Qwen3-0.6B end-to-end output tok/s.
+        del w
+        torch.cuda.empty_cache()
+        mixed, mixed_description = attention_workload("llama3_mixed", device)
+        shipped = time_attention(mixed, hip, device, args.steps, args.warmup)
+        serial = time_attention(mixed, hip, device, args.steps, args.warmup, concurrent=False)
+        record = prefill_record(mixed, serial)
+        record["workload"] = mixed_description
+        record["mixed_step_ms"] = round(shipped["ms_per_step"], 5)
+        record["mixed_step_ms_serial"] = round(serial["ms_per_step"], 5)
+        record["decode_part_frac"] = round(decode_kernel_bytes(mixed) / (serial["decode_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        result["prefill"] = record
+        del mixed
+        torch.cuda.empty_cache()
+        run = run_generation(device, "qwen3_e2e", modes=("sync", "pipelined"))
+        sync, pipelined = run["modes"]["sync"], run["modes"]["pipelined"]
+        result["e2e"] = {
+            "workload": run["workload"],
+            "value": sync["output_tok_s"],
+            "unit": "output tok/s",
+            "timing": "synchronized engine steps summed (benchmarks/benchmark_engine.py:305-315)",
+            "value_pipelined": pipelined["output_tok_s"],
+            "sync": sync,
+            "pipelined": pipelined,
+        }
     print(json.dumps(result), flush=True)
     return 0
 

@@ -17,7 +17,12 @@ Scheduling follows the reference Scheduler's semantics (core/scheduler.py):
   (stop tokens are ignored).
 
 Blocks come from a pool whose last id is the null block that pads block
-tables (core/block.py:39; model_runner.py:243-245). The step's flattened
+tables (core/block.py:39; model_runner.py:243-245). With
+`enable_prefix_cache=True` (config.py:112) complete blocks are indexed by
+their chained digest after every step and a newly admitted request starts
+after the longest indexed run of its blocks, sharing those physical blocks
+with every other request that holds them (`block_pool.BlockPool`,
+kv_cache_manager.py:113-222, scheduler.py:124-157). The step's flattened
 input and attention metadata are built on the GPU
 (`worker.packing.pack_scheduler_output`); sampling runs on the device with
 one device-to-host copy of the sampled token ids per step.
@@ -49,7 +54,9 @@ from dataclasses import dataclass, field
 import torch
 
 from micro_vllm_amd.attention.spec import FullAttentionSpec
+from micro_vllm_amd.harness.block_pool import BlockPool
 from micro_vllm_amd.harness.model import DecoderModel
+from micro_vllm_amd.harness.prefix_hash import BlockHashChain
 from micro_vllm_amd.worker.packing import allocate_packed_batch, pack_scheduler_output
 from micro_vllm_amd.worker.scheduler_output import (
     CacheGroupBlockTable,
@@ -71,6 +78,19 @@ class Request:
         # Prompt followed by the outputs, grown in place (no per-step copies).
         self.token_ids: list[int] = list(self.prompt_token_ids) + list(self.output_token_ids)
         self._block_tuple: tuple[int, ...] | None = None
+        # Prefix cache: digests of the complete blocks, and how many of the
+        # request's leading blocks are indexed (or were a cache hit).
+        self.hash_chain: BlockHashChain | None = None
+        self.cached_blocks = 0
+
+    def num_resolved_tokens(self) -> int:
+        """Leading tokens that are real ids (pipelined mode appends
+        placeholders for tokens still on the GPU, always at the end)."""
+
+        n = len(self.token_ids)
+        while n and self.token_ids[n - 1] < 0:
+            n -= 1
+        return n
 
     def append_output(self, token: int) -> None:
         self.output_token_ids.append(token)
@@ -100,6 +120,7 @@ class GenerationResult:
     preemptions: int
     decode_steps: int = 0          # steps whose requests all decode one token
     decode_seconds: float = 0.0
+    prefix_hit_tokens: int = 0     # prompt tokens served by the prefix cache
 
     @property
     def output_tokens_per_second(self) -> float:
@@ -120,6 +141,8 @@ class GenerationEngine:
         max_model_len: int = 8192,
         decode_graphs: bool = False,
         pipeline: bool = False,
+        enable_prefix_cache: bool = False,
+        cache_namespace: str = "harness",
     ) -> None:
         c = model.config
         self.model = model
@@ -139,7 +162,10 @@ class GenerationEngine:
             )
             for _ in range(c.num_hidden_layers)
         ]
-        self._free_blocks = deque(range(num_blocks - 1))
+        self.pool = BlockPool(num_blocks)
+        self.enable_prefix_cache = enable_prefix_cache
+        self.cache_namespace = cache_namespace
+        self.prefix_hit_tokens = 0
         self._waiting: deque[Request] = deque()
         self._running: list[Request] = []
         self._requests: dict[str, Request] = {}
@@ -168,15 +194,62 @@ class GenerationEngine:
         needed = -(-num_tokens // self.block_size) - len(request.block_ids)
         if needed <= 0:
             return True
-        if needed > len(self._free_blocks):
+        new = self.pool.allocate(needed)
+        if new is None:
             return False
-        request.block_ids.extend(self._free_blocks.popleft() for _ in range(needed))
+        request.block_ids.extend(new)
         return True
 
     def _free(self, request: Request) -> None:
-        self._free_blocks.extend(request.block_ids)
+        self.pool.release_all(request.block_ids)
         request.block_ids = []
         request._block_tuple = None
+        request.cached_blocks = 0
+
+    def _chain(self, request: Request) -> BlockHashChain:
+        if request.hash_chain is None:
+            request.hash_chain = BlockHashChain(
+                block_size=self.block_size, cache_namespace=self.cache_namespace, vectorized=True
+            )
+        return request.hash_chain
+
+    def _cache_hit(self, request: Request) -> list[int]:
+        """Indexed blocks of the longest prefix of the request's first
+        (known tokens - 1) // block_size blocks (kv_cache_manager.py:113-134,
+        cache_group_manager.py:235-253)."""
+
+        bs = self.block_size
+        limit = min((request.num_known_tokens - 1) // bs, request.num_resolved_tokens() // bs)
+        hit = []
+        for digest in self._chain(request).extend(request.token_ids, max(limit, 0)):
+            block = self.pool.lookup(digest)
+            if block is None:
+                break
+            hit.append(block)
+        return hit
+
+    def _commit(self, request: Request) -> None:
+        """Index the request's complete computed blocks; a block whose digest
+        is indexed under another block is replaced by that canonical block
+        (cache_group_manager.py:98-132)."""
+
+        if not self.enable_prefix_cache:
+            return
+        full = min(request.num_computed_tokens, request.num_resolved_tokens()) // self.block_size
+        if full <= request.cached_blocks:
+            return
+        digests = self._chain(request).extend(request.token_ids, full)
+        for i in range(request.cached_blocks, full):
+            block, digest = request.block_ids[i], digests[i]
+            canonical = self.pool.lookup(digest)
+            if canonical is None:
+                self.pool.index(block, digest)
+            elif canonical != block:
+                self.pool.acquire(canonical)
+                request.block_ids[i] = canonical
+                self.pool.release(block)
+                request._block_tuple = None
+        request.cached_blocks = full
 
     # ----------------------------------------------------------- schedule
     def _scheduled(self, request: Request, num_tokens: int) -> ScheduledRequest:
@@ -228,11 +301,19 @@ class GenerationEngine:
             and len(self._running) < self.max_num_seqs
         ):
             request = self._waiting[0]
-            n = min(request.num_known_tokens, budget)
-            if not self._ensure_blocks(request, n):
+            hit = self._cache_hit(request) if self.enable_prefix_cache else []
+            computed = len(hit) * self.block_size
+            n = min(request.num_known_tokens - computed, budget, self.max_model_len - computed)
+            new = self.pool.allocate(-(-(computed + n) // self.block_size) - len(hit), hit)
+            if new is None:
                 if not scheduled:
                     raise RuntimeError(f"request {request.request_id} cannot fit in the KV cache")
                 break
+            request.block_ids = hit + new
+            request._block_tuple = None
+            request.num_computed_tokens = computed
+            request.cached_blocks = len(hit)
+            self.prefix_hit_tokens += computed
             scheduled.append(self._scheduled(request, n))
             budget -= n
             self._waiting.popleft()
@@ -246,9 +327,10 @@ class GenerationEngine:
             request.num_computed_tokens += item.num_scheduled_tokens
             if item.requires_sampling:
                 request.append_output(next(samples))
-                if request.finished:
-                    self._running.remove(request)
-                    self._free(request)
+            self._commit(request)
+            if item.requires_sampling and request.finished:
+                self._running.remove(request)
+                self._free(request)
 
     # ---------------------------------------------------------------- step
     @torch.inference_mode()
@@ -324,6 +406,7 @@ class GenerationEngine:
             preemptions=self.preemptions,
             decode_steps=decode_steps,
             decode_seconds=decode_seconds,
+            prefix_hit_tokens=self.prefix_hit_tokens,
         )
 
     # ------------------------------------------------------- pipelining
@@ -336,6 +419,7 @@ class GenerationEngine:
             request.num_computed_tokens += 1
             request.append_output(-(1 + row))
             step.slots.append((request, len(request.output_token_ids) - 1))
+            self._commit(request)
             if request.finished:
                 self._running.remove(request)
                 self._free(request)

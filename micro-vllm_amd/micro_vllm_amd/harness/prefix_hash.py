@@ -83,24 +83,60 @@ def block_hashes(
 
 
 class BlockHashChain:
-    """One request's block digests, extended as its blocks fill up."""
+    """One request's block digests, extended as its blocks fill up.
 
-    __slots__ = ("block_size", "cache_namespace", "cache_group_id", "hashes")
+    With ``vectorized=True`` a block's token ids are encoded in one numpy
+    call and fed to a copy of a digest primed with the fixed header: the same
+    bytes in the same order, so the digests are identical to ``hash_block``'s
+    (blake2b of a concatenation does not depend on how it is split into
+    updates)."""
 
-    def __init__(self, *, block_size: int, cache_namespace: str, cache_group_id: int = 0) -> None:
+    __slots__ = ("block_size", "cache_namespace", "cache_group_id", "hashes", "_header")
+
+    def __init__(
+        self, *, block_size: int, cache_namespace: str, cache_group_id: int = 0, vectorized: bool = False
+    ) -> None:
         self.block_size = block_size
         self.cache_namespace = cache_namespace
         self.cache_group_id = cache_group_id
         self.hashes: list[bytes] = []
+        self._header = None
+        if vectorized:
+            namespace = cache_namespace.encode("utf-8")
+            header = blake2b(digest_size=BLOCK_HASH_BYTES, person=_HASH_DOMAIN)
+            header.update(len(namespace).to_bytes(8, "big"))
+            header.update(namespace)
+            header.update(cache_group_id.to_bytes(8, "big"))
+            header.update(block_size.to_bytes(8, "big"))
+            self._header = header
 
     def extend(self, token_ids: Sequence[int], num_blocks: int) -> tuple[bytes, ...]:
         """The first ``num_blocks`` digests; only blocks not hashed before are
         hashed now. ``token_ids`` must extend the tokens of earlier calls (a
-        request's tokens only grow; a preempted request starts a new chain)."""
+        request's tokens only grow), and every token of the hashed blocks must
+        be a real (non-negative) id."""
 
         bs = self.block_size
         parent = self.hashes[-1] if self.hashes else None
-        for b in range(len(self.hashes), num_blocks):
+        first = len(self.hashes)
+        if self._header is not None and num_blocks > first:
+            block_bytes = np.asarray(token_ids[first * bs : num_blocks * bs], dtype=">i8")
+            if block_bytes.size and block_bytes.min() < 0:
+                raise ValueError("cannot hash a block that holds a negative token id")
+            raw = block_bytes.tobytes()
+            width = 8 * bs
+            for i, b in enumerate(range(first, num_blocks)):
+                digest = self._header.copy()
+                if parent is None:
+                    digest.update(b"\x00")
+                else:
+                    digest.update(b"\x01")
+                    digest.update(parent)
+                digest.update(raw[i * width : (i + 1) * width])
+                parent = digest.digest()
+                self.hashes.append(parent)
+            return tuple(self.hashes[:num_blocks])
+        for b in range(first, num_blocks):
             parent = hash_block(
                 parent,
                 token_ids[b * bs : (b + 1) * bs],

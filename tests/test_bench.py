@@ -106,3 +106,18 @@ def test_torch_baseline_leaves_tokens_outside_requests_zero_and_empty_rows_nan()
     assert torch.all(out[-1] == 0)
     assert torch.isnan(out[17]).all()
     assert torch.isfinite(out[18]).all()
+
+
+def test_cpu_baseline_runs_the_reference_cpu_path_on_every_host_thread():
+    import torch
+
+    sys.path.insert(0, str(ROOT / "micro-vllm_amd"))
+    from micro_vllm_amd import workloads
+
+    w = workloads.small_mixed("cpu", dtype=torch.bfloat16)
+    before = w.cache.clone()
+    r = bench.cpu_baseline(w, sample_requests=4, repeats=2, warmups=1)
+    assert r["kind"] == "port" and r["unit"] == "GB/s" and r["value"] > 0
+    assert r["cores"] == bench.host_threads() >= 1
+    assert "4 of 4 sequences" in r["sample"] and r["cpu_model"]
+    assert torch.equal(w.cache, before)  # the baseline works on a host copy

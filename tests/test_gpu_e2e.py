@@ -50,8 +50,9 @@ def make_requests(seed, count, lo, hi, max_tokens, vocab=VOCAB):
 
 
 @torch.inference_mode()
-def teacher_forced_logits(model, sequences, device):
-    """Logits of every position of each sequence (one prefill step)."""
+def teacher_forced_logits(model, sequences, device, last=None):
+    """Logits of every position of each sequence (one prefill step); with
+    ``last`` only those of each sequence's last ``last[i]`` positions."""
 
     plan_items, block, tables = [], 0, []
     for i, seq in enumerate(sequences):
@@ -70,6 +71,10 @@ def teacher_forced_logits(model, sequences, device):
     )
     hidden = model.forward(packed.input_ids, packed.positions, caches, packed.group_metadata[0])
     del caches
+    if last is not None:
+        ends = np.cumsum([len(seq) for seq in sequences])
+        rows = np.concatenate([np.arange(e - k, e) for e, k in zip(ends, last)])
+        hidden = hidden.index_select(0, torch.as_tensor(rows, device=hidden.device))
     return model.logits(hidden).float()
 
 
@@ -78,16 +83,16 @@ def check_against_reference(requests, hip_model, ref_model, device):
     identical greedy tokens, on a margin the test verifies."""
 
     sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in requests]
-    ref_logits = teacher_forced_logits(ref_model, sequences, device)
-    hip_logits = teacher_forced_logits(hip_model, sequences, device)
+    last = [len(r.output_token_ids) for r in requests]
+    ref_logits = teacher_forced_logits(ref_model, sequences, device, last)
+    hip_logits = teacher_forced_logits(hip_model, sequences, device, last)
     assert torch.isfinite(hip_logits).all()
     max_diff = (hip_logits - ref_logits).abs().max().item()
 
     offset, checked, min_gap, divergence = 0, 0, float("inf"), None
-    for r, seq in zip(requests, sequences):
-        first = len(r.prompt_token_ids) - 1
-        rows = ref_logits[offset + first : offset + len(seq)]
-        offset += len(seq)
+    for r, k in zip(requests, last):
+        rows = ref_logits[offset : offset + k]
+        offset += k
         top2 = rows.topk(2, dim=-1)
         expected = top2.indices[:, 0].tolist()
         gap = (top2.values[:, 0] - top2.values[:, 1]).tolist()
@@ -300,3 +305,47 @@ def test_random_init_logits_agree_at_qwen3_0_6b_shape(device):
     assert torch.isfinite(hip).all()
     assert diff.max().item() < 0.25
     assert diff.mean().item() < 0.01
+
+
+LLAMA3_VOCAB = 128_256
+
+
+def test_llama3_shared_prefix_with_preemption_greedy_tokens_match_reference(device):
+    """The Llama-3-8B end-to-end configuration's pattern at reduced depth: the
+    Llama-3-8B layer shape (hidden 4096, 32/8 heads of 128, MLP 14,336, vocab
+    128,256), 2 layers. Six requests share a 4,096-token random prefix, each
+    followed by its own suffix of U[100, 500] tokens; prefix caching on
+    (config.py:112), so the prefix is computed once and every later request
+    is admitted at the computed offset 4,096 on the same physical blocks
+    (kv_cache_manager.py:113-134); a 512-token budget chunks every prefill;
+    a 359-block pool cannot hold every running request, so older requests
+    preempt newer ones (scheduler.py:100-113), which are later re-admitted
+    onto the shared prefix. 64 greedy tokens per request, each equal to the
+    reference-semantics operator's."""
+
+    hip_model, ref_model = models(
+        device, seed=31, fused_layers=True, base=DecoderConfig.llama3_8b, num_hidden_layers=2, vocab_size=LLAMA3_VOCAB
+    )
+    rng = np.random.default_rng(31)
+    prefix = rng.integers(0, LLAMA3_VOCAB, size=4096).tolist()
+    requests = [
+        Request(f"r{i}", prefix + rng.integers(0, LLAMA3_VOCAB, size=int(rng.integers(100, 501))).tolist(), 64)
+        for i in range(6)
+    ]
+    engine = GenerationEngine(
+        hip_model,
+        num_blocks=360,
+        max_num_batched_tokens=512,
+        max_num_seqs=8,
+        max_model_len=8192,
+        decode_graphs=True,
+        pipeline=True,
+        enable_prefix_cache=True,
+        cache_namespace="llama3-shape",
+    )
+    result = engine.generate(requests)
+    print(f"steps {result.steps}, preemptions {result.preemptions}, prefix-cache hit tokens {result.prefix_hit_tokens}")
+    assert result.output_tokens == 6 * 64
+    assert result.preemptions > 0
+    assert result.prefix_hit_tokens >= (5 + result.preemptions) * 4096
+    assert check_against_reference(requests, hip_model, ref_model, device) == 6 * 64

@@ -324,3 +324,71 @@ def test_ragged_config1_batch_matches_dense():
         np.testing.assert_allclose(out[cursor : cursor + queries[r]], expected, atol=2e-5, rtol=1e-5)
         cursor += queries[r]
     assert not np.isnan(out).any()
+
+
+# ------------------------------- the torch CPU path (bench's CPU baseline)
+
+
+def _torch_call(torch, q, k, v, cache, batch):
+    from oracle import reference_cpu
+
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    return reference_cpu.reference_forward(
+        t(q), t(k), t(v), cache,
+        t(batch.query_positions), t(batch.query_context_start_positions), t(batch.query_start_locations),
+        t(batch.context_lengths), t(batch.block_table), t(batch.slot_mapping), batch.block_size,
+    )
+
+
+@pytest.mark.parametrize("c", GOLDEN["attention_cases"], ids=lambda c: c["name"])
+def test_torch_cpu_path_matches_reference_vectors(c):
+    torch = pytest.importorskip("torch")
+    dtype = np.float16 if c["dtype"] == "float16" else np.float32
+    cache = torch.from_numpy(cache_from_case(c, dtype))
+    batch = batch_from_case(c)
+    out = _torch_call(torch, np.array(c["query"], dtype), np.array(c["key"], dtype), np.array(c["value"], dtype), cache, batch)
+    np.testing.assert_allclose(out.double().numpy(), np.array(c["expect_output"]), atol=c["tolerance"], rtol=0)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_torch_cpu_path_matches_the_oracle_on_a_ragged_gqa_batch(dtype):
+    """A 40-token chunk at offset 20, two decodes and a 3-token chunk, 8 q /
+    2 KV heads, head_dim 16, block 4, shuffled blocks: the cache after the
+    write is bit-identical and the outputs agree to fp32 rounding."""
+
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    lengths, qlens = [60, 9, 33, 5], [40, 1, 1, 3]
+    need = [-(-L // 4) for L in lengths]
+    pool = rng.permutation(sum(need) + 2)
+    tables, cursor = [], 0
+    for n in need:
+        tables.append(pool[cursor : cursor + n].tolist())
+        cursor += n
+    num_blocks = len(pool) + 1
+    positions = [list(range(L - q, L)) for L, q in zip(lengths, qlens)]
+    batch = oracle.make_batch(positions, tables, block_size=4, null_block_id=num_blocks - 1)
+    n = sum(qlens)
+    tdt = torch.float32 if dtype == "float32" else torch.bfloat16
+    q = torch.randn(n, 8, 16).to(tdt)
+    k = torch.randn(n, 2, 16).to(tdt)
+    v = torch.randn(n, 2, 16).to(tdt)
+    cache = torch.randn(2, num_blocks, 4, 2, 16).to(tdt)
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()  # noqa: E731
+    np_cache = bits(cache).copy()
+    oracle.write_kv_cache(bits(k), bits(v), np_cache, batch.slot_mapping)
+    expected = oracle.reference_forward(
+        oracle.to_f32(bits(q)), oracle.to_f32(bits(k)), oracle.to_f32(bits(v)), oracle.to_f32(np_cache), batch
+    )
+    out = _torch_call(torch, bits(q), bits(k), bits(v), cache, batch) if dtype == "float32" else None
+    if dtype == "bfloat16":
+        from oracle import reference_cpu
+
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+        out = reference_cpu.reference_forward(
+            q, k, v, cache, t(batch.query_positions), t(batch.query_context_start_positions),
+            t(batch.query_start_locations), t(batch.context_lengths), t(batch.block_table), t(batch.slot_mapping), 4,
+        )
+    assert np.array_equal(bits(cache), np_cache)
+    tol = 1e-5 if dtype == "float32" else 8e-3  # bf16 output rounding
+    np.testing.assert_allclose(out.float().numpy(), expected, atol=tol, rtol=tol)

@@ -62,6 +62,19 @@ def test_incremental_chain_equals_from_scratch_chains():
     assert chain.extend(tokens, 3) == want[:3]
 
 
+def test_vectorized_chain_gives_the_same_digests():
+    rng = np.random.default_rng(4)
+    tokens = rng.integers(0, 2**40, size=500).tolist()
+    plain = BlockHashChain(block_size=16, cache_namespace="model-a", cache_group_id=1)
+    fast = BlockHashChain(block_size=16, cache_namespace="model-a", cache_group_id=1, vectorized=True)
+    for n in (0, 15, 16, 48, 49, 300, 500):
+        assert fast.extend(tokens[:n], n // 16) == plain.extend(tokens[:n], n // 16)
+    known = BlockHashChain(block_size=4, cache_namespace="model-a", vectorized=True)
+    assert known.extend((1, 2, 3, 4), 1)[0].hex() == "fe7ca7b417786c985f1887b3d0ac9dace5ab4cbb74e201f115d7ee22cd15a52e"
+    with pytest.raises(ValueError):
+        BlockHashChain(block_size=4, cache_namespace="m", vectorized=True).extend((1, 2, -3, 4), 1)
+
+
 def test_measure_step_cost_reports_both_paths():
     r = measure_step_cost([100, 300], steps=2)
     assert r["requests"] == 2 and r["full_blocks"] == 100 // 16 + 300 // 16
