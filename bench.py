@@ -412,7 +412,10 @@ def run_generation(device, workload: str, *, modes=("sync",), requests: int | No
             for size in engine.graphs.BUCKETS:
                 if size <= spec["max_num_seqs"]:
                     engine.graphs.capture(size)
-        result = engine.generate([Request(f"r{i}", p, max_tokens=spec["max_tokens"]) for i, p in enumerate(prompts)])
+        print(f"[bench] {workload} {mode}: generating", file=sys.stderr, flush=True)
+        result = engine.generate(
+            [Request(f"r{i}", p, max_tokens=spec["max_tokens"]) for i, p in enumerate(prompts)], progress_seconds=20.0
+        )
         records[mode] = {
             "output_tok_s": round(result.output_tokens_per_second, 2),
             "steps": result.steps,

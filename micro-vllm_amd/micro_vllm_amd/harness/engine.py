@@ -47,6 +47,7 @@ placeholders are filled in.
 
 from __future__ import annotations
 
+import sys
 import time
 from collections import deque
 from dataclasses import dataclass, field
@@ -354,7 +355,7 @@ class GenerationEngine:
         logits = self.model.logits(hidden.index_select(0, rows))
         return logits.argmax(dim=-1).tolist()
 
-    def generate(self, requests: list[Request]) -> GenerationResult:
+    def generate(self, requests: list[Request], progress_seconds: float | None = None) -> GenerationResult:
         """Run every request to completion. Synchronous mode times the
         synchronized steps (schedule + execute + update, as the reference
         benchmark times Engine.step, benchmarks/benchmark_engine.py:312-315);
@@ -369,7 +370,12 @@ class GenerationEngine:
         torch.cuda.synchronize(device)
         pending: PendingStep | None = None
         loop_start = time.perf_counter()
+        next_report = loop_start + progress_seconds if progress_seconds else None
         while self.has_unfinished_requests():
+            if next_report is not None and time.perf_counter() >= next_report:
+                done = sum(len(r.output_token_ids) for r in requests)
+                print(f"[generate] step {steps}, {done} output tokens, {len(self._running)} running", file=sys.stderr, flush=True)
+                next_report += progress_seconds
             start = time.perf_counter()
             plan = self.schedule()
             if self.pipeline and self.graphs.accepts(plan):
