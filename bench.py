@@ -350,7 +350,8 @@ E2E_CONFIGS = {
 
 
 def run_generation(device, workload: str, *, modes=("sync",), requests: int | None = None,
-                   max_tokens: int | None = None, unfused: bool = False, seed: int = 0) -> dict:
+                   max_tokens: int | None = None, unfused: bool = False, seed: int = 0,
+                   full_block_lists: bool = False) -> dict:
     """Greedy generation with a random-init decoder through the harness
     engine. ``modes``: "sync" times synchronized steps and sums them (the
     reference's method, benchmarks/benchmark_engine.py:305-315: each step is
@@ -405,6 +406,7 @@ def run_generation(device, workload: str, *, modes=("sync",), requests: int | No
             pipeline=mode == "pipelined",
             enable_prefix_cache=spec["prefix_cache"],
             cache_namespace=spec["model"],
+            incremental_block_table=not full_block_lists,
         )
         if engine.graphs is not None:
             # Capture every bucket before timing (the reference captures at
@@ -433,6 +435,7 @@ def run_generation(device, workload: str, *, modes=("sync",), requests: int | No
             ),
             "preemptions": result.preemptions,
             "prefix_hit_tokens": result.prefix_hit_tokens,
+            "host_pack_ms_per_step": round(result.pack_seconds / max(result.steps, 1) * 1e3, 4),
             "output_tokens": result.output_tokens,
             "prompt_tokens": result.prompt_tokens,
         }
@@ -450,6 +453,7 @@ def run_generation(device, workload: str, *, modes=("sync",), requests: int | No
         f"max_num_seqs {spec['max_num_seqs']}, block 16, {num_blocks} KV blocks"
         + (", prefix cache on" if spec["prefix_cache"] else "")
         + ("; torch layers" if unfused else "; fused HIP layer kernels")
+        + ("; full block lists sent every step" if full_block_lists else "; device-resident block table (deltas)")
     )
     return {"workload": description, "parameters": model.parameter_count(), "modes": records}
 
@@ -565,7 +569,7 @@ def e2e_line(args, device) -> dict:
         modes = ("sync",)
     run = run_generation(
         device, args.workload, modes=modes, requests=args.e2e_requests, max_tokens=args.e2e_max_tokens,
-        unfused=args.e2e_unfused,
+        unfused=args.e2e_unfused, full_block_lists=args.e2e_full_block_lists,
     )
     rec = run["modes"][modes[0]]
     return {
@@ -612,6 +616,11 @@ def main() -> int:
         "--e2e-pipelined",
         action="store_true",
         help="end-to-end with the host one graph step ahead (the loop's wall time instead of summed steps)",
+    )
+    parser.add_argument(
+        "--e2e-full-block-lists",
+        action="store_true",
+        help="end-to-end packing that re-sends every request's block list each step (no device-resident table)",
     )
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=5)

@@ -272,8 +272,11 @@ int mvllm_context_starts(const int64_t* positions, int64_t num_tokens,
  *   request_info[r * 8 + 1] = num_scheduled_tokens
  *   request_info[r * 8 + 2] = number of block ids of request r (this group)
  *   request_info[r * 8 + 3] = 1 if the request requires sampling, else 0
- *   request_info[r * 8 + 4 .. 7] = scratch, overwritten by the call (the
+ *   request_info[r * 8 + 4 .. 5] = scratch, overwritten by the call (the
  *                                  per-request prefix sums)
+ *   request_info[r * 8 + 6] = the request's row of a device-resident block
+ *                             table (mvllm_pack_batch_rows only)
+ *   request_info[r * 8 + 7] = unused
  *   block_ids   = concatenation of every request's block ids (this group)
  *   token_ids   = concatenation of every request's input token ids (may be
  *                 NULL when input_ids is NULL)
@@ -321,6 +324,38 @@ typedef struct mvllm_pack_args {
 #define MVLLM_PACK_FIELDS 8
 
 int mvllm_pack_batch(const mvllm_pack_args* args, void* stream);
+
+/*
+ * A device-resident copy of every live request's block ids, kept across
+ * steps and updated by deltas (no counterpart in the reference, whose
+ * ModelRunner rebuilds the table from full Python lists with one host-to-
+ * device copy per request row every step, model_runner.py:871-900):
+ *   rows[slot * width + i] = block id i of the request that owns `slot`;
+ *   updates = num_updates records of 4 int32 each, (slot, first, count,
+ *             offset): rows[slot * width + first + j] = block_ids[offset + j]
+ *             for j < count, where block_ids is the pack call's payload.
+ */
+typedef struct mvllm_block_rows {
+  int32_t* rows;
+  int64_t num_slots;
+  int64_t width;
+  const int32_t* updates;
+  int64_t num_updates;
+} mvllm_block_rows;
+
+/*
+ * mvllm_pack_batch over a device-resident block table: the call first
+ * applies `rows`' updates (args->block_ids / num_block_ids hold only the
+ * updated ids), then packs as mvllm_pack_batch does, reading request r's
+ * block ids from rows[request_info[r * 8 + 6] * width ...]
+ * (request_info[r * 8 + 2] of them; a slot out of range or a list longer
+ * than `width` is an error the kernels turn into null / -1 entries).
+ * Single cache group per call. Replaces the per-step table rebuild of
+ * ModelRunner._build_block_table / _build_slot_mapping (model_runner.py:
+ * 833-900) for a caller that knows which block ids changed.
+ */
+int mvllm_pack_batch_rows(const mvllm_pack_args* args,
+                          const mvllm_block_rows* rows, void* stream);
 
 /*
  * Fused residual add + RMSNorm over `rows` rows of `dim` bf16/fp16 values

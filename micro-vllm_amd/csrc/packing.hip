@@ -26,9 +26,32 @@ __device__ __forceinline__ int64_t spec_start(int32_t kind, int64_t param, int64
   return 0;
 }
 
-__global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(mvllm_pack_args a) {
+// Device-resident block rows (mvllm_pack_batch_rows); rows == nullptr: the
+// block ids of every request are in the payload.
+struct Rows {
+  int32_t* rows;
+  int64_t num_slots, width;
+  const int32_t* updates;
+  int64_t num_updates;
+};
+
+__global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(mvllm_pack_args a, Rows rw) {
   __shared__ int64_t tok[kScanThreads], blk[kScanThreads], smp[kScanThreads];
   const int tid = threadIdx.x;
+  // Row updates first: the fill kernel that follows reads the rows. Each
+  // record is range-checked; a bad one is skipped.
+  if (rw.rows) {
+    for (int64_t u = 0; u < rw.num_updates; ++u) {
+      const int32_t* rec = rw.updates + 4 * u;
+      const int64_t slot = rec[0], first = rec[1], count = rec[2], offset = rec[3];
+      if (slot < 0 || slot >= rw.num_slots || first < 0 || count < 0 || first + count > rw.width ||
+          offset < 0 || offset + count > a.num_block_ids)
+        continue;
+      int32_t* dst = rw.rows + slot * rw.width + first;
+      for (int64_t i = tid; i < count; i += kScanThreads) dst[i] = a.block_ids[offset + i];
+    }
+    __syncthreads();
+  }
   int64_t carry_tok = 0, carry_blk = 0, carry_smp = 0;
   for (int64_t base = 0; base < a.num_requests; base += kScanThreads) {
     const int64_t r = base + tid;
@@ -77,7 +100,7 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(mvllm_pack_args
       a.query_start_locations[i] = a.num_tokens;
 }
 
-__global__ __launch_bounds__(kFillThreads) void pack_fill_kernel(mvllm_pack_args a,
+__global__ __launch_bounds__(kFillThreads) void pack_fill_kernel(mvllm_pack_args a, Rows rw,
                                                                 int64_t pad_blocks) {
   const int tid = threadIdx.x;
   const int64_t R = a.num_requests;
@@ -85,9 +108,18 @@ __global__ __launch_bounds__(kFillThreads) void pack_fill_kernel(mvllm_pack_args
   if (static_cast<int64_t>(blockIdx.x) < R) {
     const int64_t r = blockIdx.x;
     const int32_t* info = a.request_info + r * MVLLM_PACK_FIELDS;
-    const int64_t computed = info[0], scheduled = info[1], nblocks = info[2];
+    const int64_t computed = info[0], scheduled = info[1];
+    int64_t nblocks = info[2];
     const int64_t t0 = info[4], b0 = info[5];
     const int32_t* ids = a.block_ids + b0;
+    if (rw.rows) {
+      // A request's ids come from its row; an out-of-range slot or a list
+      // longer than the row has no block ids (null entries, slot -1).
+      const int64_t slot = info[6];
+      const bool ok = slot >= 0 && slot < rw.num_slots && nblocks <= rw.width;
+      ids = rw.rows + (ok ? slot : 0) * rw.width;
+      if (!ok) nblocks = 0;
+    }
     for (int64_t i = tid; i < scheduled; i += kFillThreads) {
       const int64_t t = t0 + i;
       const int64_t pos = computed + i;
@@ -162,10 +194,22 @@ extern "C" int mvllm_context_starts(const int64_t* positions, int64_t num_tokens
   return MVLLM_OK;
 }
 
-extern "C" int mvllm_pack_batch(const mvllm_pack_args* args, void* stream) {
-  clear_error();
+namespace mvllm {
+namespace {
+
+int pack_batch(const mvllm_pack_args* args, const mvllm_block_rows* rows, void* stream) {
   if (!args) return fail(MVLLM_ERR_INVALID, "pack args are null");
   const mvllm_pack_args& a = *args;
+  Rows rw = {nullptr, 0, 0, nullptr, 0};
+  if (rows) {
+    if (!rows->rows || rows->num_slots <= 0 || rows->width <= 0)
+      return fail(MVLLM_ERR_INVALID, "block rows need a table of positive size");
+    if (rows->num_updates < 0 || (rows->num_updates > 0 && !rows->updates))
+      return fail(MVLLM_ERR_INVALID, "block-row updates are null");
+    if (rows->num_slots > INT32_MAX || rows->width > INT32_MAX)
+      return fail(MVLLM_ERR_INVALID, "block rows too large");
+    rw = Rows{rows->rows, rows->num_slots, rows->width, rows->updates, rows->num_updates};
+  }
   if (int rc = check_spec(a.spec_kind, a.spec_parameter)) return rc;
   if (a.num_requests < 0 || a.num_tokens < 0 || a.num_block_ids < 0 || a.block_size <= 0 ||
       a.block_table_width < 0)
@@ -180,7 +224,7 @@ extern "C" int mvllm_pack_batch(const mvllm_pack_args* args, void* stream) {
     return fail(MVLLM_ERR_INVALID, "input_ids requested without token_ids");
   if (a.num_requests > INT32_MAX / 2) return fail(MVLLM_ERR_INVALID, "too many requests");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a);
+  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, a, rw);
   MVLLM_LAUNCH_CHECK("pack_scan_kernel");
   const int64_t pad_elems = std::max<int64_t>(
       std::max<int64_t>(a.token_capacity - a.num_tokens, a.request_capacity - a.num_requests),
@@ -189,7 +233,22 @@ extern "C" int mvllm_pack_batch(const mvllm_pack_args* args, void* stream) {
   if (pad_blocks < 1) pad_blocks = 1;
   if (pad_blocks > 1024) pad_blocks = 1024;
   hipLaunchKernelGGL(pack_fill_kernel, dim3(static_cast<unsigned>(a.num_requests + pad_blocks)),
-                     dim3(kFillThreads), 0, s, a, pad_blocks);
+                     dim3(kFillThreads), 0, s, a, rw, pad_blocks);
   MVLLM_LAUNCH_CHECK("pack_fill_kernel");
   return MVLLM_OK;
+}
+
+}  // namespace
+}  // namespace mvllm
+
+extern "C" int mvllm_pack_batch(const mvllm_pack_args* args, void* stream) {
+  clear_error();
+  return pack_batch(args, nullptr, stream);
+}
+
+extern "C" int mvllm_pack_batch_rows(const mvllm_pack_args* args, const mvllm_block_rows* rows,
+                                     void* stream) {
+  clear_error();
+  if (!rows) return fail(MVLLM_ERR_INVALID, "block rows are null");
+  return pack_batch(args, rows, stream);
 }

@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_gather_kv",
     "mvllm_context_starts",
     "mvllm_pack_batch",
+    "mvllm_pack_batch_rows",
     "mvllm_add_rms_norm",
     "mvllm_qk_norm_rope_kv_write",
     "mvllm_silu_mul",
@@ -133,6 +134,16 @@ class PackArgs(ctypes.Structure):
     ]
 
 
+class BlockRows(ctypes.Structure):
+    _fields_ = [
+        ("rows", _ptr),
+        ("num_slots", _i64),
+        ("width", _i64),
+        ("updates", _ptr),
+        ("num_updates", _i64),
+    ]
+
+
 class Timing(ctypes.Structure):
     _fields_ = [
         ("decode_start", _ptr),
@@ -186,6 +197,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mvllm_context_starts.restype = ctypes.c_int
     lib.mvllm_pack_batch.argtypes = [p(PackArgs), _ptr]
     lib.mvllm_pack_batch.restype = ctypes.c_int
+    lib.mvllm_pack_batch_rows.argtypes = [p(PackArgs), p(BlockRows), _ptr]
+    lib.mvllm_pack_batch_rows.restype = ctypes.c_int
     lib.mvllm_add_rms_norm.argtypes = [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int32, _ptr]
     lib.mvllm_add_rms_norm.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope_kv_write.argtypes = [

@@ -58,7 +58,7 @@ from micro_vllm_amd.attention.spec import FullAttentionSpec
 from micro_vllm_amd.harness.block_pool import BlockPool
 from micro_vllm_amd.harness.model import DecoderModel
 from micro_vllm_amd.harness.prefix_hash import BlockHashChain
-from micro_vllm_amd.worker.packing import allocate_packed_batch, pack_scheduler_output
+from micro_vllm_amd.worker.packing import DeviceBlockRows, allocate_packed_batch, pack_scheduler_output
 from micro_vllm_amd.worker.scheduler_output import (
     CacheGroupBlockTable,
     ScheduledRequest,
@@ -83,6 +83,10 @@ class Request:
         # request's leading blocks are indexed (or were a cache hit).
         self.hash_chain: BlockHashChain | None = None
         self.cached_blocks = 0
+        # Device-resident block table: how many of block_ids the request's
+        # row holds, and the first entry replaced since (None: none).
+        self.row_sent = 0
+        self.row_dirty: int | None = None
 
     def num_resolved_tokens(self) -> int:
         """Leading tokens that are real ids (pipelined mode appends
@@ -122,6 +126,7 @@ class GenerationResult:
     decode_steps: int = 0          # steps whose requests all decode one token
     decode_seconds: float = 0.0
     prefix_hit_tokens: int = 0     # prompt tokens served by the prefix cache
+    pack_seconds: float = 0.0      # host time spent packing steps (payload + launches)
 
     @property
     def output_tokens_per_second(self) -> float:
@@ -144,6 +149,7 @@ class GenerationEngine:
         pipeline: bool = False,
         enable_prefix_cache: bool = False,
         cache_namespace: str = "harness",
+        incremental_block_table: bool = True,
     ) -> None:
         c = model.config
         self.model = model
@@ -167,6 +173,11 @@ class GenerationEngine:
         self.enable_prefix_cache = enable_prefix_cache
         self.cache_namespace = cache_namespace
         self.prefix_hit_tokens = 0
+        # Each running request's block ids live in a device row updated by
+        # deltas (created on the first packed step).
+        self.incremental_block_table = incremental_block_table
+        self.block_rows: DeviceBlockRows | None = None
+        self.pack_seconds = 0.0
         self._waiting: deque[Request] = deque()
         self._running: list[Request] = []
         self._requests: dict[str, Request] = {}
@@ -206,6 +217,10 @@ class GenerationEngine:
         request.block_ids = []
         request._block_tuple = None
         request.cached_blocks = 0
+        if self.block_rows is not None:
+            self.block_rows.release(request.request_id)
+        request.row_sent = 0
+        request.row_dirty = None
 
     def _chain(self, request: Request) -> BlockHashChain:
         if request.hash_chain is None:
@@ -250,6 +265,7 @@ class GenerationEngine:
                 request.block_ids[i] = canonical
                 self.pool.release(block)
                 request._block_tuple = None
+                request.row_dirty = i if request.row_dirty is None else min(request.row_dirty, i)
         request.cached_blocks = full
 
     # ----------------------------------------------------------- schedule
@@ -334,6 +350,38 @@ class GenerationEngine:
                 self._free(request)
 
     # ---------------------------------------------------------------- step
+    def pack(self, plan: SchedulerOutput, into=None):
+        """Pack a step on the GPU. With the incremental block table only the
+        block ids that changed since a request's row was last written travel."""
+
+        start = time.perf_counter()
+        kwargs = {}
+        if self.incremental_block_table:
+            if self.block_rows is None:
+                self.block_rows = DeviceBlockRows(
+                    self.max_num_seqs, -(-self.max_model_len // self.block_size), self.model.device
+                )
+            updates = []
+            for item in plan.scheduled_requests:
+                request = self._requests[item.request_id]
+                first = request.row_sent if request.row_dirty is None else min(request.row_sent, request.row_dirty)
+                n = len(request.block_ids)
+                if first < n:
+                    updates.append((request.request_id, first, request.block_ids[first:n]))
+                request.row_sent, request.row_dirty = n, None
+            kwargs = dict(block_rows=self.block_rows, row_updates=updates)
+        packed = pack_scheduler_output(
+            plan,
+            specs=[FullAttentionSpec()],
+            block_size=self.block_size,
+            null_block_id=self.null_block_id,
+            device=self.model.device,
+            into=into,
+            **kwargs,
+        )
+        self.pack_seconds += time.perf_counter() - start
+        return packed
+
     @torch.inference_mode()
     def execute(self, plan: SchedulerOutput) -> list[int]:
         """One model step on the GPU; returns the greedy tokens of the
@@ -341,13 +389,7 @@ class GenerationEngine:
 
         if self.graphs is not None and self.graphs.accepts(plan):
             return self.graphs.run(plan)
-        packed = pack_scheduler_output(
-            plan,
-            specs=[FullAttentionSpec()],
-            block_size=self.block_size,
-            null_block_id=self.null_block_id,
-            device=self.model.device,
-        )
+        packed = self.pack(plan)
         hidden = self.model.forward(packed.input_ids, packed.positions, self.kv_caches, packed.group_metadata[0])
         rows = packed.sampling_row_indices
         if rows.numel() == 0:
@@ -413,6 +455,7 @@ class GenerationEngine:
             decode_steps=decode_steps,
             decode_seconds=decode_seconds,
             prefix_hit_tokens=self.prefix_hit_tokens,
+            pack_seconds=self.pack_seconds,
         )
 
     # ------------------------------------------------------- pipelining
@@ -488,15 +531,7 @@ class DecodeGraphs:
         return min(b for b in self.BUCKETS if b >= num_requests)
 
     def _pack(self, plan: SchedulerOutput, buffers) -> None:
-        e = self.engine
-        pack_scheduler_output(
-            plan,
-            specs=[FullAttentionSpec()],
-            block_size=e.block_size,
-            null_block_id=e.null_block_id,
-            device=e.model.device,
-            into=buffers,
-        )
+        self.engine.pack(plan, into=buffers)
 
     def forward(self, buffers) -> tuple[torch.Tensor, torch.Tensor]:
         """The decode step on a bucket's buffers: logits and greedy token of every row."""

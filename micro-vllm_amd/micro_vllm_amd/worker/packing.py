@@ -41,6 +41,49 @@ class PackedBatch:
     sampling_row_indices: torch.Tensor
 
 
+class DeviceBlockRows:
+    """A device-resident copy of every live request's block ids, updated by
+    deltas (``mvllm_pack_batch_rows``).
+
+    The reference's ModelRunner rebuilds each step's block table from the
+    scheduler's full per-request lists, with one host-to-device copy per row
+    (model_runner.py:871-900); the list-based ``pack_scheduler_output``
+    still re-sends every id. Here each running request owns a row of
+    ``rows`` ([num_slots, width] int32 on the device) for as long as it holds
+    blocks, and a step sends only the ids that changed since the row was last
+    written: blocks appended since, or entries replaced (the prefix cache's
+    switch to a canonical block). The caller keeps that bookkeeping (it knows
+    which ids changed) and passes ``(request_id, first, ids)`` updates."""
+
+    def __init__(self, num_slots: int, width: int, device: torch.device | str) -> None:
+        if num_slots <= 0 or width <= 0:
+            raise ValueError("block rows need a positive slot count and width")
+        self.num_slots = num_slots
+        self.width = width
+        self.rows = torch.full((num_slots, width), -1, dtype=torch.int32, device=torch.device(device))
+        self._free = list(range(num_slots - 1, -1, -1))
+        self._slot_of: dict[str, int] = {}
+
+    def slot(self, request_id: str) -> int:
+        """The request's row, assigned on first use."""
+
+        slot = self._slot_of.get(request_id)
+        if slot is None:
+            if not self._free:
+                raise RuntimeError(f"no free block row for request {request_id!r} ({self.num_slots} rows)")
+            slot = self._free.pop()
+            self._slot_of[request_id] = slot
+        return slot
+
+    def has_slot(self, request_id: str) -> bool:
+        return request_id in self._slot_of
+
+    def release(self, request_id: str) -> None:
+        slot = self._slot_of.pop(request_id, None)
+        if slot is not None:
+            self._free.append(slot)
+
+
 def pack_scheduler_output(
     plan: SchedulerOutput,
     *,
@@ -52,6 +95,8 @@ def pack_scheduler_output(
     request_capacity: int | None = None,
     block_table_width: int | None = None,
     into: PackedBatch | None = None,
+    block_rows: DeviceBlockRows | None = None,
+    row_updates: Sequence[tuple[str, int, Sequence[int]]] = (),
 ) -> PackedBatch:
     """Pack ``plan`` for every cache group (``specs[g]`` is group g's spec).
 
@@ -64,6 +109,10 @@ def pack_scheduler_output(
     reading the same buffers while every step re-packs them. The returned
     batch then shares those tensors (its sampling rows are a prefix view of
     ``into.sampling_row_indices``).
+
+    With ``block_rows`` (one cache group) the block ids come from the
+    device-resident rows after ``row_updates`` are applied; only the length
+    of each request's block list is read from the plan.
     """
 
     device = torch.device(device)
@@ -108,24 +157,45 @@ def pack_scheduler_output(
     if num_tokens + 1 > np.iinfo(np.int32).max:
         raise ValueError("too many tokens for the int32 payload")
 
-    # Host payload: [token ids | per group: request info, block ids].
+    if block_rows is not None and num_groups != 1:
+        raise ValueError("device-resident block rows serve one cache group")
+
+    # Host payload: [token ids | per group: request info, block ids] and,
+    # with block rows, [update records] at the end.
     segments = [
         np.fromiter(chain.from_iterable(r.input_token_ids for r in requests), dtype=np.int32, count=num_tokens)
     ]
     group_layout = []
     widths = []
     offset = num_tokens
+    update_records = None
     for g in range(num_groups):
         lengths = np.fromiter((len(r.block_tables[g].block_ids) for r in requests), dtype=np.int64, count=num_requests)
-        total_blocks = int(lengths.sum())
         info = np.zeros((num_requests, _native.PACK_FIELDS), dtype=np.int32)
         info[:, 0] = computed
         info[:, 1] = scheduled
         info[:, 2] = lengths
         info[:, 3] = sampling
-        ids = np.fromiter(
-            chain.from_iterable(r.block_tables[g].block_ids for r in requests), dtype=np.int32, count=total_blocks
-        )
+        if block_rows is None:
+            total_blocks = int(lengths.sum())
+            ids = np.fromiter(
+                chain.from_iterable(r.block_tables[g].block_ids for r in requests), dtype=np.int32, count=total_blocks
+            )
+        else:
+            if num_requests and int(lengths.max()) > block_rows.width:
+                raise ValueError(f"a block list is longer than the block rows' width {block_rows.width}")
+            info[:, 6] = np.fromiter((block_rows.slot(r.request_id) for r in requests), dtype=np.int32,
+                                     count=num_requests)
+            counts = [len(u[2]) for u in row_updates]
+            total_blocks = sum(counts)
+            ids = np.fromiter(chain.from_iterable(u[2] for u in row_updates), dtype=np.int32, count=total_blocks)
+            update_records = np.zeros((len(row_updates), 4), dtype=np.int32)
+            ids_offset = 0
+            for i, ((request_id, first, _), n) in enumerate(zip(row_updates, counts)):
+                if first < 0 or first + n > block_rows.width:
+                    raise ValueError(f"row update of {request_id!r} exceeds the block rows' width")
+                update_records[i] = (block_rows.slot(request_id), first, n, ids_offset)
+                ids_offset += n
         max_len = int(lengths.max()) if num_requests else 0
         width = max_len if block_table_width is None else block_table_width
         if width < max_len:
@@ -134,6 +204,9 @@ def pack_scheduler_output(
         group_layout.append((offset, offset + info.size, total_blocks))
         segments.extend((info.reshape(-1), ids))
         offset += info.size + total_blocks
+    updates_offset = offset
+    if update_records is not None:
+        segments.append(update_records.reshape(-1))
     host = torch.from_numpy(np.concatenate(segments) if segments else np.zeros(0, np.int32))
     if host.numel() == 0:
         host = torch.zeros(1, dtype=torch.int32)
@@ -194,7 +267,16 @@ def pack_scheduler_output(
         args.block_table = block_table.data_ptr() if block_table.numel() else None
         args.slot_mapping = slot_mapping.data_ptr() if token_capacity else None
         args.sampling_rows = sampling_rows.data_ptr() if first and num_sampling else None
-        _native.check(lib.mvllm_pack_batch(args, stream), "mvllm_pack_batch")
+        if block_rows is None:
+            _native.check(lib.mvllm_pack_batch(args, stream), "mvllm_pack_batch")
+        else:
+            rows = _native.BlockRows()
+            rows.rows = block_rows.rows.data_ptr()
+            rows.num_slots = block_rows.num_slots
+            rows.width = block_rows.width
+            rows.updates = base + 4 * updates_offset if len(row_updates) else None
+            rows.num_updates = len(row_updates)
+            _native.check(lib.mvllm_pack_batch_rows(args, rows, stream), "mvllm_pack_batch_rows")
     # `payload` was allocated on the current stream, so the caching allocator
     # reuses its memory only for work ordered after these launches.
     return PackedBatch(

@@ -60,11 +60,14 @@ def test_struct_sizes_match_the_header_layout():
     assert ctypes.sizeof(_native.Batch) == 6 * 8 + 3 * 8 + 2 * 8 + 8 + 8
     assert ctypes.sizeof(_native.PackArgs) == 3 * 8 + 5 * 8 + 8 + 4 * 8 + 8 * 8
     assert ctypes.sizeof(_native.Timing) == 4 * 8
+    assert ctypes.sizeof(_native.BlockRows) == 8 + 2 * 8 + 8 + 8
 
 
 def test_library_rejects_bad_arguments_without_a_device():
     lib = _native.load()
     assert lib.mvllm_pack_batch(None, None) == _native.ERR_INVALID
+    assert lib.mvllm_pack_batch_rows(None, None, None) == _native.ERR_INVALID
+    assert b"rows" in lib.mvllm_last_error()
     assert b"null" in lib.mvllm_last_error()
     assert lib.mvllm_context_starts(None, 4, 7, 0, None, None) == _native.ERR_INVALID
     assert b"spec" in lib.mvllm_last_error()

@@ -349,3 +349,26 @@ def test_llama3_shared_prefix_with_preemption_greedy_tokens_match_reference(devi
     assert result.preemptions > 0
     assert result.prefix_hit_tokens >= (5 + result.preemptions) * 4096
     assert check_against_reference(requests, hip_model, ref_model, device) == 6 * 64
+
+
+def test_duplicate_prompts_share_canonical_blocks_through_the_device_block_table(device):
+    """Two identical prompts admitted in the same step compute their blocks
+    twice; the prefix cache then switches the second request to the first
+    one's blocks (cache_group_manager.py:98-132) and the device-resident
+    block table receives only those replaced entries. Decoding continues on
+    the shared blocks (graphs, pipelined): both requests produce the same
+    tokens, equal to the reference's."""
+
+    hip_model, ref_model = models(device, seed=41, fused_layers=True)
+    rng = np.random.default_rng(41)
+    prompt = rng.integers(0, VOCAB, size=300).tolist()
+    other = rng.integers(0, VOCAB, size=200).tolist()
+    requests = [Request("a", list(prompt), 24), Request("b", list(prompt), 24), Request("c", other, 24)]
+    engine = GenerationEngine(
+        hip_model, num_blocks=128, max_num_batched_tokens=1024, max_num_seqs=4, max_model_len=512,
+        decode_graphs=True, pipeline=True, enable_prefix_cache=True,
+    )
+    result = engine.generate(requests)
+    assert result.outputs["a"] == result.outputs["b"]
+    assert engine.pool.num_cached_blocks >= 300 // 16
+    check_against_reference(requests, hip_model, ref_model, device)

@@ -180,3 +180,59 @@ def test_build_metadata_keeps_inputs_and_computes_starts(device):
     big = torch.arange(0, 1_000_000, 7, device=device)
     got = context_starts(big, ChunkedLocalSpec(13)).cpu().numpy()
     assert np.array_equal(got, oracle.context_starts(oracle.CHUNKED_LOCAL, 13, big.cpu().numpy()))
+
+
+# ------------------------------------------ device-resident block rows (deltas)
+
+
+def test_device_block_rows_give_the_oracle_packing_over_steps(device):
+    """A device-resident block table updated by deltas (appended ids,
+    a replaced entry, a released row reused by another request) packs every
+    step bit-identically to the oracle packing of the full lists, unpadded
+    and at graph capacities."""
+
+    from micro_vllm_amd.worker.packing import DeviceBlockRows, allocate_packed_batch
+
+    rng = np.random.default_rng(12)
+    rows = DeviceBlockRows(num_slots=4, width=48, device=device)
+    null = 999
+    lists = {"a": rng.permutation(500)[:20].tolist(), "b": rng.permutation(500)[:3].tolist()}
+    sent = {"a": 0, "b": 0}
+    computed = {"a": 300, "b": 40}
+    steps = [
+        dict(),                                   # both rows written from scratch
+        dict(append={"a": 1}),                    # one appended id
+        dict(replace={"a": 5}),                   # a replaced entry (prefix-cache dedup)
+        dict(release="b", admit=("c", 7)),        # b leaves, c takes its row
+        dict(append={"c": 2, "a": 1}),
+    ]
+    buffers = allocate_packed_batch(num_groups=1, block_size=16, token_capacity=8, request_capacity=4,
+                                    block_table_widths=[48], sampling_capacity=4, device=device, max_query_len=4)
+    for step in steps:
+        updates = []
+        for rid, n in step.get("append", {}).items():
+            lists[rid].extend(rng.integers(500, 900, size=n).tolist())
+        for rid, i in step.get("replace", {}).items():
+            lists[rid][i] = 901
+            sent[rid] = min(sent[rid], i)
+        if "release" in step:
+            rows.release(step["release"])
+            del lists[step["release"]], computed[step["release"]]
+            rid, n = step["admit"]
+            lists[rid], sent[rid], computed[rid] = rng.permutation(500)[:n].tolist(), 0, 90
+        for rid, ids in lists.items():
+            if sent[rid] < len(ids):
+                updates.append((rid, sent[rid], ids[sent[rid]:]))
+                sent[rid] = len(ids)
+        requests = []
+        for rid, ids in lists.items():
+            q = 1 if rid != "c" else 3
+            pos0 = min(computed[rid], len(ids) * 16 - q)
+            requests.append(oracle.Request(rid, tuple(range(q)), pos0, q, True, (tuple(ids),)))
+        plan = plan_from(requests)
+        for into, caps in ((None, None), (buffers, dict(token_capacity=8, request_capacity=4, block_table_width=48))):
+            packed = pack_scheduler_output(plan, specs=[FullAttentionSpec()], block_size=16, null_block_id=null,
+                                           device=device, into=into, block_rows=rows, row_updates=updates)
+            torch.cuda.synchronize()
+            check_against_oracle(packed, requests, [FullAttentionSpec()], block_size=16, null_block_id=null, capacities=caps)
+            updates = []  # the rows already hold them for the padded pass
