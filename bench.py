@@ -622,6 +622,11 @@ def main() -> int:
         action="store_true",
         help="end-to-end packing that re-sends every request's block list each step (no device-resident table)",
     )
+    parser.add_argument(
+        "--no-hint",
+        action="store_true",
+        help="attention metadata without the max_query_len hint (the reference's AttentionMetadata fields only)",
+    )
     parser.add_argument("--cpu-sample", type=int, default=256, help="sequences timed by the CPU baseline")
     parser.add_argument("--cpu-repeats", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -659,6 +664,11 @@ def main() -> int:
         return 0
 
     w, description = attention_workload(args.workload, device)
+    if args.no_hint:
+        import dataclasses
+
+        w.metadata = dataclasses.replace(w.metadata, max_query_len=None)
+        description += "; metadata without the max_query_len hint"
     torch.cuda.synchronize()
     hip = HipEvents()
     timing = time_attention(w, hip, device, args.steps, args.warmup)

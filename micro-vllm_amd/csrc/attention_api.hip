@@ -4,7 +4,7 @@
 #include <cstdlib>
 #include <mutex>
 
-#include "attention.h"
+#include "worklists.h"
 
 namespace mvllm {
 
@@ -173,6 +173,30 @@ SideStream* side_stream(hipStream_t caller) {
   return &ss;
 }
 
+// The fused prologue of a forward: workgroup 0 builds the decode work list
+// and the per-request table, workgroup 1 (when the batch may hold
+// multi-query requests) the prefill work list, and every later workgroup
+// copies the K/V rows of `rows_per_wg` tokens into their cache slots. One
+// launch instead of three: the lists depend only on the metadata, never on
+// the cache, so they may be built while the rows are written.
+constexpr int kPrologueThreads = 1024;
+static_assert(kPrologueThreads == kDecodeListThreads && kPrologueThreads == kItemThreads,
+              "the list builders run on one full prologue workgroup");
+
+__global__ __launch_bounds__(kPrologueThreads) void forward_prologue_kernel(AttnArgs a, KvRowArgs kv,
+                                                                            int32_t lg_tok, int32_t lists,
+                                                                            int32_t rows_per_wg) {
+  const int64_t wg = blockIdx.x;
+  if (wg < lists) {
+    if (wg == 0) build_decode_list(a);
+    else build_prefill_list(a, lg_tok);
+    return;
+  }
+  const int span = kPrologueThreads / rows_per_wg;  // threads per token row
+  const int64_t token = (wg - lists) * rows_per_wg + threadIdx.x / span;
+  if (token < a.num_tokens) copy_kv_row(kv, token, threadIdx.x % span, span);
+}
+
 // Batch and cache fields of the kernel arguments.
 void fill_batch_args(AttnArgs& a, const mvllm_batch* batch, const mvllm_kv_cache* cache, int64_t Hq) {
   a.cache = cache->data;
@@ -203,6 +227,20 @@ bool fast_cache(const mvllm_kv_cache* cache, int64_t group) {
   return (dtype == MVLLM_DTYPE_BF16 || dtype == MVLLM_DTYPE_F16) && cache->head_dim == 128 && group <= 16 &&
          cache->stride[4] == 1 && cache->stride[3] == cache->head_dim && vec16(cache->stride[0], es) &&
          vec16(cache->stride[1], es) && vec16(cache->stride[2], es) && aligned16(cache->data);
+}
+
+// The MFMA decode / prefill path (with work lists) applies: 16-byte aligned
+// rows of query, output and cache, head_dim 128, a supported group size and
+// at least one request; otherwise the generic kernel runs.
+bool attention_fast_path(const mvllm_tensor3* query, const mvllm_kv_cache* cache, const mvllm_tensor3* out,
+                         const mvllm_batch* batch) {
+  if (!query || !cache || !out || !batch || batch->num_requests <= 0) return false;
+  const int64_t Hkv = cache->num_kv_heads;
+  if (Hkv <= 0 || query->size[1] % Hkv != 0) return false;
+  const int64_t es = dtype_bytes(query->dtype);
+  return fast_cache(cache, query->size[1] / Hkv) && query->stride[2] == 1 && vec16(query->stride[0], es) &&
+         vec16(query->stride[1], es) && aligned16(query->data) && out->stride[2] == 1 &&
+         vec16(out->stride[0], es) && vec16(out->stride[1], es) && aligned16(out->data);
 }
 
 // Split-KV partials, work lists and the per-request table in the workspace.
@@ -245,7 +283,8 @@ int attention_plan(const mvllm_batch* batch, int64_t Hq, const mvllm_kv_cache* c
 int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
                     const mvllm_batch* batch, const mvllm_tensor3* out, float scale,
                     void* workspace, int64_t workspace_bytes, const mvllm_timing* timing,
-                    void* stream, bool planned = false, bool single_stream = false) {
+                    void* stream, bool planned = false, bool single_stream = false,
+                    const KvRowArgs* fused_kv = nullptr) {
   if (int rc = check_tensor(query, "query")) return rc;
   if (int rc = check_tensor(out, "out")) return rc;
   if (!cache || !cache->data) return fail(MVLLM_ERR_INVALID, "cache is null");
@@ -276,22 +315,47 @@ int paged_attention(const mvllm_tensor3* query, const mvllm_kv_cache* cache,
   a.scale_log2 = scale * 1.4426950408889634f;  // log2(e)
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
-  const int64_t es = dtype_bytes(dtype);
-  const bool fast = fast_cache(cache, a.group) && query->stride[2] == 1 && vec16(query->stride[0], es) &&
-                    vec16(query->stride[1], es) && aligned16(query->data) && out->stride[2] == 1 &&
-                    vec16(out->stride[0], es) && vec16(out->stride[1], es) && aligned16(out->data);
-  if (!fast || a.num_requests == 0) {
+  const bool fast = attention_fast_path(query, cache, out, batch);
+  if (!fast) {
+    if (fused_kv) {
+      // Only the rows: the generic kernel needs no work lists.
+      const int64_t blocks = ceil_div(N, 1);
+      hipLaunchKernelGGL(forward_prologue_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kPrologueThreads), 0, s,
+                         a, *fused_kv, 0, 0, 1);
+      MVLLM_LAUNCH_CHECK("forward_prologue_kernel");
+    }
     a.mode = 0;
     return launch_generic(a, dtype, s);
   }
   if (int rc = bind_workspace(a, batch, Hq, D, workspace, workspace_bytes)) return rc;
   a.lists_ready = planned ? 1 : 0;
+  const bool wants_prefill = batch->max_query_len != 1 && prefill_supported(a, dtype);
+  if (fused_kv) {
+    // The step's K/V rows and the work lists in one launch; the decode and
+    // prefill launches below then find the lists ready.
+    const int64_t chunks2 = 2 * static_cast<int64_t>(fused_kv->chunks);
+    int32_t rows_per_wg = 1;
+    while (rows_per_wg < 64 && 2 * rows_per_wg * chunks2 <= kPrologueThreads) rows_per_wg *= 2;
+    if (chunks2 > kPrologueThreads) rows_per_wg = 1;
+    const int32_t lists = a.lists_ready ? 0 : (wants_prefill ? 2 : 1);
+    if (a.lists_ready) {
+      // Lists were planned: only the rows (the planned decode launch checks its reach).
+    } else if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX) {
+      return fail(MVLLM_ERR_UNSUPPORTED, "decode positions beyond 2^31 are not supported");
+    }
+    const int64_t blocks = lists + ceil_div(N, rows_per_wg);
+    if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "prologue grid too large");
+    hipLaunchKernelGGL(forward_prologue_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kPrologueThreads), 0, s,
+                       a, *fused_kv, static_cast<int32_t>(prefill_lg_tok(a)), lists, rows_per_wg);
+    MVLLM_LAUNCH_CHECK("forward_prologue_kernel");
+    a.lists_ready = 1;
+  }
   hipEvent_t ds = timing ? static_cast<hipEvent_t>(timing->decode_start) : nullptr;
   hipEvent_t de = timing ? static_cast<hipEvent_t>(timing->decode_stop) : nullptr;
   hipEvent_t ps = timing ? static_cast<hipEvent_t>(timing->prefill_start) : nullptr;
   hipEvent_t pe = timing ? static_cast<hipEvent_t>(timing->prefill_stop) : nullptr;
   // A batch known to hold only single-query requests needs no prefill launch.
-  if (batch->max_query_len != 1 && prefill_supported(a, dtype)) {
+  if (wants_prefill) {
     // A fork and join cost ~10 us: the prefill moves to the side stream only
     // when the hint says that the batch holds multi-query requests.
     SideStream* side = batch->max_query_len > 1 && !single_stream ? side_stream(s) : nullptr;
@@ -325,6 +389,15 @@ int attention_forward(const mvllm_tensor3* query, const mvllm_tensor3* key,
   if (!batch) return fail(MVLLM_ERR_INVALID, "batch is null");
   if (batch->num_tokens > 0) {
     if (!batch->slot_mapping) return fail(MVLLM_ERR_INVALID, "slot_mapping is null");
+    KvRowArgs rows;
+    bool vectorised = false;
+    if (int rc = kv_write_prepare(key, value, cache, batch->slot_mapping, batch->num_tokens, &rows, &vectorised))
+      return rc;
+    // The fused prologue needs the attention's MFMA path (the work lists)
+    // and 16-byte rows; everything else writes the rows first, on its own.
+    if (vectorised && attention_fast_path(query, cache, out, batch))
+      return paged_attention(query, cache, batch, out, scale, workspace, workspace_bytes, timing, stream, false,
+                             single_stream, &rows);
     if (int rc = mvllm_kv_write(key, value, cache, batch->slot_mapping, batch->num_tokens, stream))
       return rc;
   }

@@ -33,7 +33,7 @@
 
 #include <hip/hip_ext.h>
 
-#include "attention.h"
+#include "worklists.h"
 
 namespace mvllm {
 namespace {
@@ -604,122 +604,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
 }
 
 
-// ---- decode work list --------------------------------------------------------
-//
-// One workgroup lists the (request, split) items of the single-query
-// requests: every full split first (in any order), then the partial last
-// splits from the largest down, so the in-order dispatch of the decode grid
-// ends on the shortest items. Empty slots (up to R * max_splits) get
-// request -1.
-constexpr int kDecodeListThreads = 1024;
-constexpr int kSizeBuckets = 64;  // sizes of a partial split, split / 64 tokens (rounded up to a power of two) each
-
-__global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnArgs a) {
-  __shared__ int32_t full_count, full_pos;
-  __shared__ int32_t bucket[kSizeBuckets];
-  const int tid = threadIdx.x;
-  const int64_t R = a.num_requests;
-  const int64_t capacity = R * a.max_splits;
-  // 64 buckets of 2^bucket_shift sizes span every split length: the
-  // smallest shift with 64 << shift >= split_tokens (a partial split holds
-  // 1 .. split_tokens - 1 keys, so its bucket index stays below 64).
-  int bucket_shift = 0;
-  while ((kSizeBuckets << bucket_shift) < a.split_tokens) ++bucket_shift;
-  if (tid == 0) full_count = full_pos = 0;
-  if (tid < kSizeBuckets) bucket[tid] = 0;
-  // A decode request: its query token, visible keys, split count and the
-  // size of its last split (ns = 0: not a decode request, or no visible key;
-  // dec = 1 marks a decode request).
-  struct Desc {
-    int32_t qs, lo, hi, ns, last, dec;
-  };
-  auto describe = [&](int64_t r) {
-    Desc d = {0, 0, -1, 0, 0, 0};
-    const int64_t qs = a.qsl[r];
-    if (qs < 0 || qs >= a.num_tokens || a.qsl[r + 1] - qs != 1) return d;
-    d.qs = static_cast<int32_t>(qs);
-    d.dec = 1;
-    int64_t lo, hi;
-    visible_range(a, r, qs, qs, lo, hi);
-    const int64_t n = decode_num_splits(lo, hi, a.split_tokens);
-    if (n <= 0) return d;
-    d.lo = static_cast<int32_t>(lo);
-    d.hi = static_cast<int32_t>(hi);
-    d.ns = static_cast<int32_t>(n);
-    d.last = static_cast<int32_t>((hi - (lo & ~int64_t(15)) + 1) - (n - 1) * a.split_tokens);
-    return d;
-  };
-  auto record = [&](int64_t r, const Desc& d, int32_t sp) {
-    const int32_t begin = (d.lo & ~15) + sp * a.split_tokens;
-    const int32_t end = begin + a.split_tokens - 1 < d.hi ? begin + a.split_tokens - 1 : d.hi;
-    return DecodeItem{static_cast<int32_t>(r), sp, d.qs, d.ns, d.lo, d.hi, begin, end};
-  };
-  // The thread's first request stays in registers between the passes.
-  Desc d0 = {0, 0, -1, 0, 0, 0};
-  if (tid < R) d0 = describe(tid);
-  __syncthreads();
-  const int lane = tid & 63;
-  // Exclusive prefix of v over the wave and the wave's total.
-  auto wave_scan = [&](int32_t v, int32_t& total) {
-    int32_t incl = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int32_t y = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += y;
-    }
-    total = __shfl(incl, 63, 64);
-    return incl - v;
-  };
-  // Pass 1: count full splits (one LDS atomic per wave), histogram the
-  // partial ones by size. The loop bound is uniform per wave.
-  for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
-    const int64_t r = r0 + lane;
-    Desc d = {0, 0, -1, 0, 0, 0};
-    if (r < R) d = r == tid ? d0 : describe(r);
-    const int32_t ns = d.ns, last = d.last;
-    const bool partial = ns > 0 && last < a.split_tokens;
-    int32_t total;
-    wave_scan(partial ? ns - 1 : ns, total);
-    if (lane == 0 && total) atomicAdd(&full_count, total);
-    if (partial) atomicAdd(&bucket[(last - 1) >> bucket_shift], 1);
-  }
-  __syncthreads();
-  // Partial splits start after the full ones, largest bucket first: an
-  // exclusive scan over the buckets in descending order, one lane each.
-  static_assert(kSizeBuckets == 64, "one wave scans the buckets");
-  if (tid < 64) {
-    const int32_t c = bucket[63 - tid];
-    int32_t incl = c;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int32_t y = __shfl_up(incl, d, 64);
-      if (tid >= d) incl += y;
-    }
-    const int32_t fulls = full_count;
-    bucket[63 - tid] = fulls + incl - c;
-    if (tid == 63) full_count = fulls + incl;  // total number of items
-  }
-  __syncthreads();
-  // Pass 2: place the items (one LDS atomic per wave for the full splits).
-  for (int64_t r0 = tid - lane; r0 < R; r0 += kDecodeListThreads) {
-    const int64_t r = r0 + lane;
-    Desc d = {0, 0, -1, 0, 0, 0};
-    if (r < R) d = r == tid ? d0 : describe(r);
-    const int32_t ns = d.ns, last = d.last;
-    const bool partial = ns > 0 && last < a.split_tokens;
-    const int32_t nfull = partial ? ns - 1 : ns;
-    int32_t total;
-    const int32_t excl = wave_scan(nfull, total);
-    int32_t at = 0;
-    if (lane == 0 && total) at = atomicAdd(&full_pos, total);
-    at = __shfl(at, 0, 64) + excl;
-    for (int32_t sp = 0; sp < nfull; ++sp) a.decode_items[at + sp] = record(r, d, sp);
-    if (partial) a.decode_items[atomicAdd(&bucket[(last - 1) >> bucket_shift], 1)] = record(r, d, ns - 1);
-    if (r < R) a.decode_req[r] = int2{d.qs, d.dec ? ns : -1};
-  }
-  for (int64_t j = full_count + tid; j < capacity; j += kDecodeListThreads)
-    a.decode_items[j] = DecodeItem{-1, -1, 0, 0, 0, -1, 0, -1};
-}
+__global__ __launch_bounds__(kDecodeListThreads) void decode_items_kernel(AttnArgs a) { build_decode_list(a); }
 
 struct DecodeTuning {
   bool lds_pipeline;  // the global->LDS pipelined kernel (block_size % 16 == 0)

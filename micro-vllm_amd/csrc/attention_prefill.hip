@@ -42,7 +42,7 @@
 
 #include <hip/hip_ext.h>
 
-#include "attention.h"
+#include "worklists.h"
 
 namespace mvllm {
 namespace {
@@ -50,7 +50,7 @@ namespace {
 constexpr int kDim = 128;
 constexpr int kTileKeys = 64;
 constexpr int kWaves = 4;
-constexpr int kRows = kWaves * 32;                   // rows per workgroup
+static_assert(kRows == kWaves * 32, "rows per workgroup");
 constexpr int kTileBytes = kTileKeys * kDim * 2;     // one K (or V) tile: 16 KiB
 constexpr int kTablePages = 2048;                    // block ids held in LDS at a time
 constexpr int kChunkTiles = kTablePages / 4;
@@ -547,125 +547,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     }
 }
 
-// ---- prefill work list ------------------------------------------------------
-//
-// Request r's query blocks of T tokens occupy work-list slots
-// [qsl[r] / T + r, qsl[r] / T + r + ceil(n_r / T)), which never overlap and
-// stay below N / T + R. One workgroup lists every (request, block) item of
-// the multi-query requests, sorted by the number of 64-key tiles it visits,
-// heaviest first, so that the hardware's in-order dispatch of the prefill
-// grid approximates longest-processing-time-first scheduling. Empty slots
-// (single-query requests) go last as request -1. Items within a cost
-// bucket come in any order; every item writes only its own output rows.
-constexpr int kItemThreads = 1024;
-constexpr int kItemSlots = 8192;    // larger batches keep slot order (late slots first)
-constexpr int kCostBuckets = 2048;  // tiles per item, clamped
-static_assert(kCostBuckets == 2 * kItemThreads, "the bucket scan gives each thread two buckets");
-
 __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a, int32_t lg_tok) {
-  __shared__ int32_t owner[kItemSlots];
-  __shared__ uint16_t bucket_of[kItemSlots];
-  __shared__ int32_t start[kCostBuckets];
-  __shared__ int32_t wave_sums[kItemThreads / 64];
-  __shared__ int32_t total;
-  const int tid = threadIdx.x;
-  const int64_t tpb = int64_t{1} << lg_tok;
-  const int64_t R = a.num_requests;
-  const int64_t nslots = a.num_tokens / tpb + R;
-  // Record of query block b of request r (its first query is qs, its last
-  // query token qe - 1).
-  auto record = [&](int64_t r, int64_t qs, int64_t qe, int64_t b) {
-    const int64_t t0 = qs + b * tpb;
-    const int64_t t1 = t0 + tpb < qe ? t0 + tpb : qe;
-    int64_t lo0, hi0, lo1, hi1;
-    visible_range(a, r, qs, t0, lo0, hi0);
-    visible_range(a, r, qs, t1 - 1, lo1, hi1);
-    return PrefillItem{static_cast<int32_t>(r), static_cast<int32_t>(t0), static_cast<int32_t>(t1),
-                       static_cast<int32_t>(qs), static_cast<int32_t>(lo0), static_cast<int32_t>(hi1), 0, 0};
-  };
-  const PrefillItem empty = {-1, 0, 0, 0, 0, -1, 0, 0};
-  if (nslots > kItemSlots) {
-    for (int64_t j = tid; j < nslots; j += kItemThreads) {
-      int64_t rl = 0, rh = R - 1;
-      while (rl < rh) {
-        const int64_t mid = (rl + rh + 1) >> 1;
-        if (a.qsl[mid] / tpb + mid <= j) rl = mid; else rh = mid - 1;
-      }
-      const int64_t qs = a.qsl[rl], qe = a.qsl[rl + 1];
-      const int64_t b = j - (qs / tpb + rl);
-      const bool ok = qs >= 0 && qe <= a.num_tokens && qe - qs > 1 && b >= 0 && qs + b * tpb < qe;
-      a.items[nslots - 1 - j] = ok ? record(rl, qs, qe, b) : empty;
-    }
-    return;
-  }
-  for (int j = tid; j < nslots; j += kItemThreads) owner[j] = -1;
-  for (int k = tid; k < kCostBuckets; k += kItemThreads) start[k] = 0;
-  __syncthreads();
-  for (int64_t r = tid; r < R; r += kItemThreads) {
-    const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
-    if (qs < 0 || qe > a.num_tokens || qe - qs <= 1) continue;
-    const int64_t first = qs / tpb + r;
-    const int64_t nb = (qe - qs + tpb - 1) / tpb;
-    for (int64_t b = 0; b < nb && first + b < nslots; ++b) owner[first + b] = static_cast<int32_t>(r);
-  }
-  __syncthreads();
-  // Cost of an item: 64-key tiles between its first row's first visible key
-  // and its last row's last one.
-  for (int j = tid; j < nslots; j += kItemThreads) {
-    const int32_t r = owner[j];
-    if (r < 0) continue;
-    const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
-    const int64_t t0 = qs + (j - (qs / tpb + r)) * tpb;
-    const int64_t t1 = (t0 + tpb < qe ? t0 + tpb : qe) - 1;
-    int64_t lo0, hi0, lo1, hi1;
-    visible_range(a, r, qs, t0, lo0, hi0);
-    visible_range(a, r, qs, t1, lo1, hi1);
-    const int64_t tiles = hi1 >= lo0 ? (hi1 - lo0 + 64) / 64 : 0;
-    const int bucket = static_cast<int>(tiles < kCostBuckets - 1 ? tiles : kCostBuckets - 1);
-    bucket_of[j] = static_cast<uint16_t>(bucket);
-    atomicAdd(&start[bucket], 1);
-  }
-  __syncthreads();
-  // start[k] = number of items in buckets above k (exclusive scan, heaviest
-  // first). Thread t owns buckets K - 1 - 2 t and K - 2 - 2 t.
-  {
-    const int k0 = kCostBuckets - 1 - 2 * tid;
-    const int v0 = start[k0], v1 = start[k0 - 1];
-    const int own = v0 + v1;
-    int incl = own;
-    const int lane = tid & 63, w = tid >> 6;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int y = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += y;
-    }
-    if (lane == 63) wave_sums[w] = incl;
-    __syncthreads();
-    int before = 0;
-    for (int i = 0; i < w; ++i) before += wave_sums[i];
-    const int excl = before + incl - own;
-    if (tid == kItemThreads - 1) total = excl + own;
-    __syncthreads();
-    start[k0] = excl;
-    start[k0 - 1] = excl + v0;
-  }
-  __syncthreads();
-  for (int j = tid; j < nslots; j += kItemThreads) {
-    const int32_t r = owner[j];
-    if (r < 0) continue;
-    const int pos = atomicAdd(&start[bucket_of[j]], 1);
-    const int64_t qs = a.qsl[r], qe = a.qsl[r + 1];
-    a.items[pos] = record(r, qs, qe, j - (qs / tpb + r));
-  }
-  for (int64_t j = total + tid; j < nslots; j += kItemThreads) a.items[j] = empty;
+  build_prefill_list(a, lg_tok);
 }
 
-// T = kRows / G query tokens per work item.
-int prefill_lg_tok(const AttnArgs& a) {
-  int lg_tok = 0;
-  while ((kRows >> lg_tok) > a.group) ++lg_tok;
-  return lg_tok;
-}
 
 template <typename T, bool PSPLIT>
 int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent_t stop) {

@@ -5,43 +5,14 @@
 // of whole token rows (all KV heads of one token are contiguous in the
 // reference cache layout (2, blocks, block_size, heads, dim)); the generic
 // paths handle arbitrary strides element by element.
-#include "common.h"
+#include "worklists.h"
 
 namespace mvllm {
 namespace {
 
-struct WriteArgs {
-  const char* key;
-  const char* value;
-  char* cache;
-  const int64_t* slots;
-  int64_t key_token_stride;    // bytes
-  int64_t value_token_stride;  // bytes
-  int64_t plane_stride;        // bytes
-  int64_t block_stride;        // bytes
-  int64_t offset_stride;       // bytes
-  int64_t block_size;
-  int64_t num_slots;
-  int32_t chunks;              // 16-byte chunks per token row
-};
-
-// One workgroup per token: K row then V row, 16 bytes per thread step.
-__global__ __launch_bounds__(256) void kv_write_rows_kernel(WriteArgs a) {
-  const int64_t token = blockIdx.x;
-  const int64_t slot = a.slots[token];
-  if (slot < 0 || slot >= a.num_slots) return;
-  const int64_t block = slot / a.block_size;
-  const int64_t offset = slot - block * a.block_size;
-  char* dst = a.cache + block * a.block_stride + offset * a.offset_stride;
-  const char* ksrc = a.key + token * a.key_token_stride;
-  const char* vsrc = a.value + token * a.value_token_stride;
-  for (int c = threadIdx.x; c < 2 * a.chunks; c += blockDim.x) {
-    const bool is_value = c >= a.chunks;
-    const int chunk = is_value ? c - a.chunks : c;
-    const uint4 data =
-        *reinterpret_cast<const uint4*>((is_value ? vsrc : ksrc) + 16 * chunk);
-    *reinterpret_cast<uint4*>(dst + (is_value ? a.plane_stride : 0) + 16 * chunk) = data;
-  }
+// One workgroup per token: its K row then its V row.
+__global__ __launch_bounds__(256) void kv_write_rows_kernel(KvRowArgs a) {
+  copy_kv_row(a, blockIdx.x, threadIdx.x, blockDim.x);
 }
 
 struct WriteGenericArgs {
@@ -158,10 +129,11 @@ int check_cache(const mvllm_kv_cache* cache) {
 
 using namespace mvllm;
 
-extern "C" int mvllm_kv_write(const mvllm_tensor3* key, const mvllm_tensor3* value,
-                              const mvllm_kv_cache* cache, const int64_t* slot_mapping,
-                              int64_t num_tokens, void* stream) {
-  clear_error();
+namespace mvllm {
+
+int kv_write_prepare(const mvllm_tensor3* key, const mvllm_tensor3* value, const mvllm_kv_cache* cache,
+                     const int64_t* slot_mapping, int64_t num_tokens, KvRowArgs* rows, bool* vectorised) {
+  *vectorised = false;
   if (int rc = check_cache(cache)) return rc;
   if (!key || !value) return fail(MVLLM_ERR_INVALID, "key/value descriptor is null");
   if (num_tokens < 0) return fail(MVLLM_ERR_INVALID, "negative num_tokens");
@@ -182,7 +154,6 @@ extern "C" int mvllm_kv_write(const mvllm_tensor3* key, const mvllm_tensor3* val
   if (num_tokens > INT32_MAX) return fail(MVLLM_ERR_INVALID, "too many tokens");
   const int64_t es = dtype_bytes(cache->dtype);
   const int64_t row_bytes = H * D * es;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool rows_contiguous = key->stride[2] == 1 && key->stride[1] == D &&
                                value->stride[2] == 1 && value->stride[1] == D &&
                                cache->stride[4] == 1 && cache->stride[3] == D;
@@ -191,26 +162,44 @@ extern "C" int mvllm_kv_write(const mvllm_tensor3* key, const mvllm_tensor3* val
                       (key->stride[0] * es) % 16 == 0 && (value->stride[0] * es) % 16 == 0 &&
                       (cache->stride[0] * es) % 16 == 0 && (cache->stride[1] * es) % 16 == 0 &&
                       (cache->stride[2] * es) % 16 == 0;
-  if (vec_ok) {
-    WriteArgs a;
-    a.key = static_cast<const char*>(key->data);
-    a.value = static_cast<const char*>(value->data);
-    a.cache = static_cast<char*>(cache->data);
-    a.slots = slot_mapping;
-    a.key_token_stride = key->stride[0] * es;
-    a.value_token_stride = value->stride[0] * es;
-    a.plane_stride = cache->stride[0] * es;
-    a.block_stride = cache->stride[1] * es;
-    a.offset_stride = cache->stride[2] * es;
-    a.block_size = cache->block_size;
-    a.num_slots = cache->num_blocks * cache->block_size;
-    a.chunks = static_cast<int32_t>(row_bytes / 16);
+  if (!vec_ok) return MVLLM_OK;
+  KvRowArgs& a = *rows;
+  a.key = static_cast<const char*>(key->data);
+  a.value = static_cast<const char*>(value->data);
+  a.cache = static_cast<char*>(cache->data);
+  a.slots = slot_mapping;
+  a.key_token_stride = key->stride[0] * es;
+  a.value_token_stride = value->stride[0] * es;
+  a.plane_stride = cache->stride[0] * es;
+  a.block_stride = cache->stride[1] * es;
+  a.offset_stride = cache->stride[2] * es;
+  a.block_size = cache->block_size;
+  a.num_slots = cache->num_blocks * cache->block_size;
+  a.chunks = static_cast<int32_t>(row_bytes / 16);
+  *vectorised = true;
+  return MVLLM_OK;
+}
+
+}  // namespace mvllm
+
+extern "C" int mvllm_kv_write(const mvllm_tensor3* key, const mvllm_tensor3* value,
+                              const mvllm_kv_cache* cache, const int64_t* slot_mapping,
+                              int64_t num_tokens, void* stream) {
+  clear_error();
+  KvRowArgs a;
+  bool vec = false;
+  if (int rc = kv_write_prepare(key, value, cache, slot_mapping, num_tokens, &a, &vec)) return rc;
+  if (num_tokens == 0) return MVLLM_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (vec) {
     int threads = static_cast<int>(std::min<int64_t>(256, ceil_div(2 * a.chunks, 64) * 64));
     hipLaunchKernelGGL(kv_write_rows_kernel, dim3(static_cast<unsigned>(num_tokens)),
                        dim3(threads), 0, s, a);
     MVLLM_LAUNCH_CHECK("kv_write_rows_kernel");
     return MVLLM_OK;
   }
+  const int64_t H = cache->num_kv_heads, D = cache->head_dim;
+  const int64_t es = dtype_bytes(cache->dtype);
   WriteGenericArgs g;
   g.key = static_cast<const char*>(key->data);
   g.value = static_cast<const char*>(value->data);
