@@ -471,6 +471,11 @@ def attention_workload(name: str, device):
             "llama3_long_decode: 64 decode sequences, contexts U[8192,33280] seed 0, 32 q / 8 kv heads, "
             "head_dim 128, block 16, bf16, values N(0,1)"
         )
+    if name == "llama3_long_prefill":
+        return workloads.llama3_mixed(device, offset_range=(14336, 16384), num_decodes=0), (
+            "llama3_long_prefill: 8 prefill chunks x 512 at offsets U[14336,16384] (no decodes), "
+            "32 q / 8 kv heads, head_dim 128, block 16, bf16"
+        )
     return workloads.llama3_mixed(device), (
         "llama3_mixed: 8 prefill chunks x 512 at offsets U[0,2048] + 248 decodes U[256,8192], "
         "32 q / 8 kv heads, head_dim 128, block 16, bf16"
@@ -599,7 +604,7 @@ def main() -> int:
     parser.add_argument(
         "--workload",
         default="qwen3_decode",
-        choices=["qwen3_decode", "llama3_mixed", "llama3_long_decode", "qwen3_e2e", "llama3_e2e"],
+        choices=["qwen3_decode", "llama3_mixed", "llama3_long_prefill", "llama3_long_decode", "qwen3_e2e", "llama3_e2e"],
     )
     parser.add_argument(
         "--quick",
@@ -674,7 +679,7 @@ def main() -> int:
     timing = time_attention(w, hip, device, args.steps, args.warmup)
     ms_per_step, decode_ms = timing["ms_per_step"], timing["decode_ms"]
     overlap = None
-    if args.workload == "llama3_mixed":
+    if args.workload in ("llama3_mixed", "llama3_long_prefill"):
         # The library runs a mixed batch's prefill kernel on a second stream
         # beside the decode kernel, so their HIP-event spans overlap. The
         # step above is the shipped (overlapped) one; each kernel's roofline
@@ -732,7 +737,7 @@ def main() -> int:
         result["control_plane"] = {"prefix_hash": measure_step_cost(w.context_lengths.tolist(), steps=3)}
     if overlap is not None:
         result["overlap"] = overlap
-    if args.workload == "llama3_mixed":
+    if args.workload in ("llama3_mixed", "llama3_long_prefill"):
         result["prefill"] = prefill_record(w, serial)
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
