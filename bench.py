@@ -15,7 +15,7 @@ Reported (one JSON line on stdout):
 * ``prefill``: the prefill kernel on the Llama-3-head mixed batch (8 chunks
   of 512 + 248 decodes): causal-visible FLOPs / its mean duration, against
   the 2.5 PFLOP/s bf16 peak (serial pass), and the mixed step's time with
-  the prefill beside the decode kernel;
+  the decode and prefill workgroups in one step kernel;
 * ``e2e``: Qwen3-0.6B-shaped end-to-end output tok/s, synchronized steps
   summed (the reference's method) and, as ``value_pipelined``, with the host
   one graph step ahead;
@@ -484,9 +484,13 @@ def attention_workload(name: str, device):
 
 def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurrent: bool = True) -> dict:
     """``warmup`` untimed forwards, then ``steps`` timed ones between HIP
-    events on the launch stream; per-kernel durations from the events the
-    library records around the decode and prefill launches. ``concurrent``
-    False keeps the prefill kernel on the caller's stream."""
+    events on the launch stream. ``concurrent`` True times the shipped step:
+    for a batch with prefill work that is the one-launch step kernel (decode
+    and prefill workgroups in one grid), and the library's decode events
+    bracket it. ``concurrent`` False asks for the prefill kernel's own events
+    as well, which makes the library launch the prefill and decode kernels
+    separately on the caller's stream: the per-kernel rooflines come from
+    that pass."""
 
     import torch
 
@@ -507,7 +511,8 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
         if i is not None:
             timing = _native.Timing()
             timing.decode_start, timing.decode_stop = decode_events[2 * i], decode_events[2 * i + 1]
-            timing.prefill_start, timing.prefill_stop = prefill_events[2 * i], prefill_events[2 * i + 1]
+            if not concurrent:
+                timing.prefill_start, timing.prefill_stop = prefill_events[2 * i], prefill_events[2 * i + 1]
         return hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata, timing=timing)
 
     try:
@@ -524,7 +529,7 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
             "decode_ms": statistics.mean(hip.elapsed_ms(decode_events[2 * i], decode_events[2 * i + 1]) for i in range(steps)),
         }
         out["prefill_ms"] = None
-        if (w.metadata.max_query_len or 0) > 1:
+        if not concurrent and (w.metadata.max_query_len or 0) > 1:
             try:
                 out["prefill_ms"] = statistics.mean(
                     hip.elapsed_ms(prefill_events[2 * i], prefill_events[2 * i + 1]) for i in range(steps)
@@ -680,15 +685,15 @@ def main() -> int:
     ms_per_step, decode_ms = timing["ms_per_step"], timing["decode_ms"]
     overlap = None
     if args.workload in ("llama3_mixed", "llama3_long_prefill"):
-        # The library runs a mixed batch's prefill kernel on a second stream
-        # beside the decode kernel, so their HIP-event spans overlap. The
-        # step above is the shipped (overlapped) one; each kernel's roofline
-        # comes from a second pass with the overlap switched off.
+        # The library runs a mixed batch as one launch whose grid holds the
+        # decode and the prefill workgroups. The step above is that shipped
+        # one; each kernel's roofline comes from a second pass with the two
+        # kernels launched separately, one after the other.
         serial = time_attention(w, hip, device, args.steps, args.warmup, concurrent=False)
         decode_ms = serial["decode_ms"]
         overlap = {
             "ms_per_step_serial": round(serial["ms_per_step"], 5),
-            "note": "prefill on a second stream beside the decode kernel; kernel rooflines from the serial pass",
+            "note": "decode and prefill workgroups in one step kernel; kernel rooflines from the serial pass",
         }
 
     step_bytes = workloads.decode_bytes(w)

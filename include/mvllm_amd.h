@@ -14,11 +14,15 @@
  *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *    Calls only enqueue work: nothing synchronises with the host, no device
  *    memory is allocated, so every entry point may be recorded into a HIP
- *    graph. When mvllm_batch.max_query_len > 1, the attention entry points
- *    run the prefill kernel on a second, library-owned stream (one per
- *    device, default priority, created by the first call made outside a
- *    graph capture), forked from and joined back into `stream` within the
- *    call; MVLLM_PREFILL_CONCURRENT=0 keeps all work on `stream`.
+ *    graph. A batch that may hold multi-query requests runs its decode and
+ *    prefill workgroups in one launch on `stream` (the step kernel). Only a
+ *    caller that times the prefill kernel on its own (mvllm_timing's prefill
+ *    events), or a decode shape the step kernel does not take, gets separate
+ *    launches; with max_query_len > 1 the prefill kernel then runs on a
+ *    second, library-owned stream (one per device, default priority, created
+ *    by the first call made outside a graph capture), forked from and joined
+ *    back into `stream` within the call. MVLLM_PREFILL_CONCURRENT=0 keeps all
+ *    work on `stream`; MVLLM_STEP_KERNEL=0 turns the step kernel off.
  *  - Return value: 0 on success, a negative MVLLM_ERR_* code on failure;
  *    mvllm_last_error() then describes the failure (thread-local text).
  *  - Index tensors are int64, as in the reference (AttentionMetadata,
@@ -218,7 +222,10 @@ int mvllm_attention_forward_noalloc(const mvllm_tensor3* query,
 /*
  * Optional kernel timing for measurement: hipEvent_t handles (as void*,
  * NULL = not wanted) recorded on the launch stream immediately before and
- * after the decode kernel and the prefill kernel (hipExtLaunchKernel).
+ * after the decode kernel and the prefill kernel (hipExtLaunchKernel). With
+ * prefill events set, the decode and prefill kernels are launched
+ * separately; without them, the decode events bracket the step kernel when
+ * that runs.
  */
 typedef struct mvllm_timing {
   void* decode_start;

@@ -107,6 +107,17 @@ int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t s
                    hipEvent_t stop);
 bool prefill_supported(const AttnArgs& a, int32_t dtype);
 
+// The one-launch attention step: decode and prefill workgroups in one grid
+// (attention_prefill.hip), for batches whose decode part runs the pipelined
+// kernel with its default shape (kStepDecodeWaves waves, two stages).
+constexpr int kStepDecodeWaves = 4;
+bool decode_step_eligible(const AttnArgs& a);
+int64_t decode_step_blocks(const AttnArgs& a);  // decode workgroups of the step grid
+int launch_decode_combine(const AttnArgs& a, int32_t dtype, hipStream_t s);
+// `prefill_first`: the prefill workgroups lead the grid (else the decode ones).
+int launch_step(const AttnArgs& a, int32_t dtype, bool prefill_first, hipStream_t s, hipEvent_t start,
+                hipEvent_t stop);
+
 // Device properties used for launch shapes (cached per device).
 int device_cu_count();
 

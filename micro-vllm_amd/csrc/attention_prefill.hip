@@ -42,7 +42,7 @@
 
 #include <hip/hip_ext.h>
 
-#include "worklists.h"
+#include "decode_split.h"
 
 namespace mvllm {
 namespace {
@@ -144,8 +144,7 @@ __device__ __forceinline__ short4v lds_read_tr16(const uint8_t* p) {
 }
 
 template <typename T, bool PSPLIT>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_tok) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+__device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, uint8_t* smem, uint32_t wg) {
   uint8_t* const kbuf = smem;                   // K stages 0, 1 (16 KiB each)
   uint8_t* const vbuf = smem + 2 * kTileBytes;  // V stages 0, 1
   int32_t* const page_tbl = reinterpret_cast<int32_t*>(smem + 4 * kTileBytes);
@@ -164,8 +163,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
   const int64_t nblk = a.num_tokens / tpb + R;
   // Consecutive workgroups take the KV heads of one work item (so each XCD
   // keeps reading the same head); items come heaviest first.
-  const int h = static_cast<int>(blockIdx.x % Hkv);
-  const int64_t slot = static_cast<int64_t>(blockIdx.x / Hkv);
+  const int h = static_cast<int>(wg % Hkv);
+  const int64_t slot = static_cast<int64_t>(wg / Hkv);
   if (slot >= nblk) return;
   // The record carries the rows' tokens and the hull [first row's first
   // key, last row's last key], so the page table of that range is fetched
@@ -547,6 +546,34 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
     }
 }
 
+template <typename T, bool PSPLIT>
+__global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_tok) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  prefill_body<T, PSPLIT>(a, lg_tok, smem, blockIdx.x);
+}
+
+// The one-launch attention step: the decode and prefill workgroups of a
+// forward in one grid. The first `first` workgroups run one kind (the
+// prefill ones when `prefill_first`), the rest the other, each indexing its
+// own work list exactly as in its own kernel. A CU holds two workgroups of
+// either kind (the launch reserves the prefill kernel's LDS, which covers
+// the decode kernel's four waves of two K/V stages), so the grid needs no
+// second stream to run prefill beside decode, and a batch without prefill
+// work pays only for the prefill workgroups that find an empty record.
+static_assert(kStepDecodeWaves * 2 * 2 * dec::kTileBytes <= kLdsBytes,
+              "the step kernel's LDS must hold the decode kernel's tiles");
+
+template <typename T, bool PSPLIT>
+__global__ __launch_bounds__(256, 2) void attention_step_kernel(AttnArgs a, int32_t lg_tok, uint32_t first,
+                                                               int32_t prefill_first) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t b = blockIdx.x;
+  const bool lead = b < first;
+  const uint32_t wg = lead ? b : b - first;
+  if (lead == (prefill_first != 0)) prefill_body<T, PSPLIT>(a, lg_tok, smem, wg);
+  else dec::decode_split_lds_body<T, 2>(a, smem, wg, kStepDecodeWaves);
+}
+
 __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a, int32_t lg_tok) {
   build_prefill_list(a, lg_tok);
 }
@@ -574,6 +601,35 @@ int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEven
   hipExtLaunchKernelGGL(prefill_kernel<T, PSPLIT>, dim3(static_cast<unsigned>(blocks)), dim3(256),
                         kLdsBytes, s, start, stop, 0, a, lg_tok);
   MVLLM_LAUNCH_CHECK("prefill_kernel");
+  return MVLLM_OK;
+}
+
+template <typename T, bool PSPLIT>
+int launch_step_t(const AttnArgs& a, bool prefill_first, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
+  const int lg_tok = prefill_lg_tok(a);
+  const int64_t prefill_blocks = (a.num_tokens / (int64_t{1} << lg_tok) + a.num_requests) * a.num_kv_heads;
+  const int64_t decode_blocks = decode_step_blocks(a);
+  const int64_t first = prefill_first ? prefill_blocks : decode_blocks;
+  const int64_t blocks = prefill_blocks + decode_blocks;
+  if (blocks <= 0) return MVLLM_OK;
+  if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "attention step grid too large");
+  if (!a.items || !a.decode_items || !a.decode_req) return fail(MVLLM_ERR_INVALID, "work lists are missing");
+  if (!a.lists_ready) {
+    if (int rc = launch_decode_lists(a, s)) return rc;
+    prefill_items_kernel<<<1, kItemThreads, 0, s>>>(a, lg_tok);
+    MVLLM_LAUNCH_CHECK("prefill_items_kernel");
+  }
+  static bool raised = false;  // per instantiation; the attribute is process-wide
+  if (!raised) {
+    MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_step_kernel<T, PSPLIT>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(kLdsBytes)));
+    raised = true;
+  }
+  hipExtLaunchKernelGGL(attention_step_kernel<T, PSPLIT>, dim3(static_cast<unsigned>(blocks)), dim3(256),
+                        kLdsBytes, s, start, stop, 0, a, lg_tok, static_cast<uint32_t>(first),
+                        prefill_first ? 1 : 0);
+  MVLLM_LAUNCH_CHECK("attention_step_kernel");
   return MVLLM_OK;
 }
 
@@ -608,6 +664,18 @@ int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t s
   // input type); fp16 carries P as a hi/lo pair to meet fp16 tolerances.
   if (dtype == MVLLM_DTYPE_BF16) return launch_prefill_t<bf16_t, false>(a, s, start, stop);
   return launch_prefill_t<f16_t, true>(a, s, start, stop);
+}
+
+int launch_step(const AttnArgs& a, int32_t dtype, bool prefill_first, hipStream_t s, hipEvent_t start,
+                hipEvent_t stop) {
+  if (!prefill_supported(a, dtype) || !decode_step_eligible(a))
+    return fail(MVLLM_ERR_UNSUPPORTED, "the attention step kernel does not support this geometry");
+  if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX)
+    return fail(MVLLM_ERR_UNSUPPORTED, "decode positions beyond 2^31 are not supported");
+  int rc = dtype == MVLLM_DTYPE_BF16 ? launch_step_t<bf16_t, false>(a, prefill_first, s, start, stop)
+                                     : launch_step_t<f16_t, true>(a, prefill_first, s, start, stop);
+  if (rc) return rc;
+  return launch_decode_combine(a, dtype, s);
 }
 
 }  // namespace mvllm

@@ -47,8 +47,10 @@ placeholders are filled in.
 
 from __future__ import annotations
 
+import gc
 import sys
 import time
+import weakref
 from collections import deque
 from dataclasses import dataclass, field
 
@@ -508,7 +510,11 @@ class DecodeGraphs:
     BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
 
     def __init__(self, engine: GenerationEngine) -> None:
-        self.engine = engine
+        # A weak reference: the engine owns this object, and a cycle between
+        # them would leave the captured graphs to the cyclic collector, which
+        # may run inside a later capture, where destroying a graph and
+        # freeing its memory pool is not allowed (the process aborts).
+        self._engine = weakref.ref(engine)
         self.width = -(-engine.max_model_len // engine.block_size)
         self.max_batch = self.BUCKETS[-1]
         self.pool = torch.cuda.graph_pool_handle()
@@ -519,6 +525,13 @@ class DecodeGraphs:
         self.last_tokens = torch.zeros(self.max_batch, dtype=torch.int64, device=device)
         self._host = [torch.empty(self.max_batch, dtype=torch.int64, pin_memory=True) for _ in range(2)]
         self._flip = 0
+
+    @property
+    def engine(self) -> GenerationEngine:
+        engine = self._engine()
+        if engine is None:
+            raise RuntimeError("the engine of these decode graphs no longer exists")
+        return engine
 
     def accepts(self, plan: SchedulerOutput) -> bool:
         items = plan.scheduled_requests
@@ -570,8 +583,18 @@ class DecodeGraphs:
                 self.forward(buffers)
         torch.cuda.current_stream(e.model.device).wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, pool=self.pool):
-            logits, tokens = self.forward(buffers)
+        # Whatever dead objects still hold graphs or device memory are freed
+        # here, and the cyclic collector stays off during the capture: a
+        # graph destroyed inside another capture aborts the process.
+        gc.collect()
+        collecting = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(graph, pool=self.pool):
+                logits, tokens = self.forward(buffers)
+        finally:
+            if collecting:
+                gc.enable()
         self.last_tokens.copy_(saved_tokens)
         entry = DecodeGraph(graph, buffers, logits, tokens)
         self.entries[size] = entry

@@ -31,8 +31,15 @@ def gpu_available() -> bool:
 
 @pytest.fixture
 def device():
+    """cuda:0. After the test, dead objects are collected while no graph
+    capture is under way: a HIP graph that a reference cycle keeps alive
+    must not be destroyed inside a later test's capture."""
+
+    import gc
+
     import torch
 
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
-    return torch.device("cuda", 0)
+    yield torch.device("cuda", 0)
+    gc.collect()

@@ -371,18 +371,66 @@ def test_planned_attention_matches_per_call_lists(device, case):
 
 
 def test_prefill_beside_decode_matches_serial_step(device, monkeypatch):
-    """A mixed batch runs its prefill kernel on a second stream beside the
-    decode kernel; the outputs must equal the serial step's bit for bit, and
-    the oracle's within tolerance."""
+    """A mixed batch runs as one step kernel (decode and prefill workgroups in
+    one grid) by default, or with the step kernel off, its prefill kernel on
+    a second stream beside the decode kernel. Every form must equal the
+    serial step's outputs bit for bit, and the oracle's within tolerance."""
 
     lengths = [300, 1000, 17, 2049, 600, 5, 4000]
     qlens = [300, 1, 17, 1, 64, 1, 1]
     q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, 32, 8, 128, 16, seed=73)
     md = dataclasses.replace(md, max_query_len=max(qlens))  # the hint that enables the second stream
+    step = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
+    monkeypatch.setenv("MVLLM_STEP_KERNEL", "0")
     overlapped = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
     monkeypatch.setenv("MVLLM_PREFILL_CONCURRENT", "0")
     serial = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
     assert torch.equal(overlapped.view(torch.int16), serial.view(torch.int16))
+    assert torch.equal(step.view(torch.int16), serial.view(torch.int16))
+
+
+@pytest.mark.parametrize(
+    "dtype,hq,hkv,hint,order",
+    [
+        (torch.bfloat16, 32, 8, None, None),
+        (torch.bfloat16, 32, 8, "max", "prefill"),
+        (torch.bfloat16, 16, 8, None, "prefill"),
+        (torch.float16, 16, 8, "max", None),
+        (torch.bfloat16, 16, 2, None, None),
+        (torch.bfloat16, 16, 1, "max", None),
+        (torch.bfloat16, 24, 6, None, None),
+    ],
+)
+def test_step_kernel_matches_separate_launches(device, monkeypatch, dtype, hq, hkv, hint, order):
+    """The step kernel runs the decode and prefill kernels' own work items in
+    one grid, in either order, so its outputs equal the separate launches'
+    bit for bit: with and without the hint, fewer KV heads than the step's
+    decode waves, and fp16."""
+
+    lengths = [700, 2300, 33, 1, 4100, 90, 129]
+    qlens = [128, 1, 33, 1, 1, 90, 1]
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, hq, hkv, 128, 16, seed=91)
+    if hint == "max":
+        md = dataclasses.replace(md, max_query_len=max(qlens))
+    if order:
+        monkeypatch.setenv("MVLLM_STEP_ORDER", order)
+    step = run_and_check(q, k, v, cache.clone(), md, dtype)
+    monkeypatch.setenv("MVLLM_STEP_KERNEL", "0")
+    monkeypatch.setenv("MVLLM_PREFILL_CONCURRENT", "0")
+    separate = run_and_check(q, k, v, cache.clone(), md, dtype)
+    assert torch.equal(step.view(torch.int16), separate.view(torch.int16))
+
+
+def test_step_kernel_on_a_decode_only_batch_without_the_hint(device, monkeypatch):
+    """Without the hint a decode-only batch takes the step kernel, whose
+    prefill workgroups all find empty records; the outputs equal the hinted
+    decode-only launch's."""
+
+    lengths = [5000, 17, 300, 2048, 2049, 1]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, [1] * len(lengths), 16, 8, 128, 16, seed=93)
+    unhinted = run_and_check(q, k, v, cache.clone(), md, torch.bfloat16)
+    hinted = run_and_check(q, k, v, cache.clone(), dataclasses.replace(md, max_query_len=1), torch.bfloat16)
+    assert torch.equal(unhinted.view(torch.int16), hinted.view(torch.int16))
 
 
 def test_plan_for_other_metadata_is_rejected(device):
@@ -592,10 +640,13 @@ def test_shared_4096_token_prefix_suffix_prefill_and_decode(device, hq, hkv):
     assert torch.equal(out[:512], out[512:1024])
 
 
-def test_graph_replay_matches_eager(device):
+@pytest.mark.parametrize("step_kernel", ["2", "0"])
+def test_graph_replay_matches_eager(device, monkeypatch, step_kernel):
     q, k, v, cache, md = build_case(device, torch.bfloat16, [300, 1, 2000, 45], [1, 1, 1, 20], 16, 8, 128, 16, seed=5, nan_cache=False)
-    # With the hint, the prefill runs on the library's second stream, so the
-    # capture holds a fork and a join.
+    # By default the mixed batch runs as one step kernel. With the step kernel
+    # off and the hint given, the prefill runs on the library's second stream,
+    # so the capture holds a fork and a join.
+    monkeypatch.setenv("MVLLM_STEP_KERNEL", step_kernel)
     md = dataclasses.replace(md, max_query_len=20)
     op = operator()
     eager_cache = cache.clone()

@@ -21,6 +21,7 @@ checked through their logits (no token claim): `test_random_init_logits_*`.
 from __future__ import annotations
 
 import copy
+import weakref
 
 import numpy as np
 import pytest
@@ -147,6 +148,11 @@ def test_greedy_decoding_with_decode_graphs_matches_reference_attention(device):
     assert result.output_tokens == 7 * 16
     assert set(engine.graphs.entries) >= {8}  # decode steps ran as graphs
     check_against_reference(requests, hip_model, ref_model, device)
+    # The captured graphs go with the engine's last reference, not with a
+    # later cyclic collection (which may fall inside another capture).
+    graphs = weakref.ref(engine.graphs)
+    del engine, result
+    assert graphs() is None
 
 
 @pytest.mark.parametrize("qk_norm", [True, False], ids=["qwen3", "llama3-style"])
