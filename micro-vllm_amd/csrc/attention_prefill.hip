@@ -12,9 +12,11 @@
 // one page of K and of V per tile straight from HBM into LDS
 // (global_load_lds_dwordx4) into double-buffered K and V tiles: the loads of
 // tile k+1 are issued between the MFMAs of tile k (a burst of loads would
-// stall the issuing wave) and land before the tile's one barrier. The block
-// ids of a tile's four pages are read from an LDS copy of the block-table row
-// one iteration ahead, so no table lookup sits on the critical path. Each
+// stall the issuing wave) and land before the tile's one barrier. Each wave
+// reads its page of a tile from an LDS table of per-tile records (the page's
+// packed block id and 16-row group, and the tile's valid-page mask), filled
+// from the block table per chunk of 256 tiles, one iteration ahead, so no
+// table lookup and little scalar arithmetic sits in the tile loop. Each
 // tile is computed as two halves of 32 keys, each a full online-softmax
 // update; that keeps the live registers under the 256 of two waves per SIMD.
 //
@@ -52,10 +54,10 @@ constexpr int kTileKeys = 64;
 constexpr int kWaves = 4;
 static_assert(kRows == kWaves * 32, "rows per workgroup");
 constexpr int kTileBytes = kTileKeys * kDim * 2;     // one K (or V) tile: 16 KiB
-constexpr int kTablePages = 2048;                    // block ids held in LDS at a time
-constexpr int kChunkTiles = kTablePages / 4;
-constexpr int kDummyBytes = 1024;                    // target of loads that are switched off
-constexpr size_t kLdsBytes = 4 * kTileBytes + kTablePages * 4 + 16 * 4 + kDummyBytes;  // K, V double buffers
+constexpr int kChunkTiles = 256;                     // key tiles whose pages are held in LDS at a time
+constexpr int kTableInts = kChunkTiles * 8;          // per tile and wave: (page entry, tile's valid-page mask)
+constexpr int kDummyBytes = 4096;                    // target of V page loads that are switched off
+constexpr size_t kLdsBytes = 4 * kTileBytes + kTableInts * 4 + 16 * 4 + kDummyBytes;  // K, V double buffers
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -143,12 +145,69 @@ __device__ __forceinline__ short4v lds_read_tr16(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(p));
 }
 
+// lds_dma_load16_sbase with the LDS destination given as a wave-uniform
+// base plus an immediate, added straight into M0.
+template <int OFF>
+__device__ __forceinline__ void lds_dma_load16_m0(const void* base, uint32_t offset, uint32_t lds_base) {
+  asm volatile(
+      "s_add_u32 m0, %1, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %2"
+      :
+      : "v"(offset), "s"(lds_base), "s"(base), "i"(OFF)
+      : "memory", "m0");
+}
+
+// Load i (of four) of a 16-row page: rows 4 i .. 4 i + 3, 1 KiB further into
+// the page's LDS slot per load.
+__device__ __forceinline__ void page_load(const void* src, int i, uint32_t lane_offset, uint32_t lds_slot) {
+  if (i == 0) lds_dma_load16_m0<0>(src, lane_offset, lds_slot);
+  else if (i == 1) lds_dma_load16_m0<1024>(src, lane_offset, lds_slot);
+  else if (i == 2) lds_dma_load16_m0<2048>(src, lane_offset, lds_slot);
+  else lds_dma_load16_m0<3072>(src, lane_offset, lds_slot);
+}
+
+typedef __attribute__((address_space(3))) const short8_t lds_short8c;
+// LDS reads from a 32-bit LDS byte address (the constant part of the
+// address goes into the instruction's offset field).
+__device__ __forceinline__ short8_t lds_read_b128_at(uint32_t addr) {
+  return *reinterpret_cast<lds_short8c*>(static_cast<uintptr_t>(addr));
+}
+__device__ __forceinline__ short4v lds_read_tr16_at(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_short4v*>(static_cast<uintptr_t>(addr)));
+}
+
+// Page-table entry of the 16-key page at position pos: (block id << 4) |
+// (the page's 16-row group inside its block), or -1 for an unmapped page.
+__device__ __forceinline__ int32_t page_entry(const AttnArgs& a, int64_t r, int64_t pos) {
+  const int64_t b = block_of(a, r, pos);
+  return b >= 0 ? static_cast<int32_t>((b << 4) | ((pos % a.block_size) >> 4)) : -1;
+}
+
+// The records of key tile i of a page-table chunk, starting at key position
+// tpos: for each of its four 16-key pages (one per wave), the page entry
+// (-1 past `last` or unmapped) and the tile's valid-page mask.
+__device__ __forceinline__ void fill_tile_record(int32_t* tbl, const AttnArgs& a, int64_t r, int i, int32_t tpos,
+                                                 int32_t last) {
+  int32_t e[4];
+  uint32_t mask = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int32_t pos = tpos + 16 * w;
+    e[w] = pos <= last ? page_entry(a, r, pos) : -1;
+    mask |= e[w] >= 0 ? 1u << w : 0u;
+  }
+  int4* rec = reinterpret_cast<int4*>(tbl + 8 * i);
+  rec[0] = int4{e[0], static_cast<int32_t>(mask), e[1], static_cast<int32_t>(mask)};
+  rec[1] = int4{e[2], static_cast<int32_t>(mask), e[3], static_cast<int32_t>(mask)};
+}
+
 template <typename T, bool PSPLIT>
 __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, uint8_t* smem, uint32_t wg) {
   uint8_t* const kbuf = smem;                   // K stages 0, 1 (16 KiB each)
   uint8_t* const vbuf = smem + 2 * kTileBytes;  // V stages 0, 1
   int32_t* const page_tbl = reinterpret_cast<int32_t*>(smem + 4 * kTileBytes);
-  int32_t* const red = page_tbl + kTablePages;
+  int32_t* const red = page_tbl + kTableInts;
   uint8_t* const dummy = reinterpret_cast<uint8_t*>(red + 16);
 
   const int tid = threadIdx.x;
@@ -202,10 +261,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
   // are never looked up: their table entries may be anything).
   {
     const int32_t nt = hull_tiles < kChunkTiles ? hull_tiles : kChunkTiles;
-    for (int i = tid; i < nt * 4; i += 256) {
-      const int32_t pos = hull_base + 16 * i;
-      page_tbl[i] = pos <= hull_hi ? static_cast<int32_t>(block_of(a, r, pos)) : -1;
-    }
+    for (int i = tid; i < nt; i += 256) fill_tile_record(page_tbl, a, r, i, hull_base + kTileKeys * i, hull_hi);
   }
   // Wave-uniform bounds of the wave's rows' visible ranges.
   const int32_t w_lo_min = __builtin_amdgcn_readfirstlane(wave_min_i(nonempty ? lo_n : INT_MAX));
@@ -276,10 +332,22 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         voff[4 * u + c] = tile_off(row, dim >> 3) + 2 * (dim & 7);
       }
   }
-  const uint32_t kaddr = lds_address(kbuf);
-  const uint32_t vaddr = lds_address(vbuf);
-  const uint32_t daddr = lds_address(dummy);
-  const uint32_t bs32 = static_cast<uint32_t>(a.block_size);
+  // LDS byte addresses from the start of dynamic LDS (the static size): as
+  // plain integers they stay constants, where addresses derived from the
+  // shared array's symbol are recomputed next to each use.
+  const uint32_t lds0 = __builtin_amdgcn_groupstaticsize();
+  const uint32_t kaddr = lds0;
+  const uint32_t vaddr = lds0 + 2 * kTileBytes;
+  const uint32_t daddr = lds0 + static_cast<uint32_t>(dummy - smem);
+  uint32_t klane[8], vlane[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    klane[x] = lds0 + koff[x];
+    vlane[x] = lds0 + 2 * kTileBytes + voff[x];
+    // Opaque to the compiler, so the sums stay in registers instead of
+    // being recomputed next to every read.
+    asm volatile("" : "+v"(klane[x]), "+v"(vlane[x]));
+  }
   // Byte offsets within a 16-row page segment of the page loads: instruction
   // i covers rows 4 i .. 4 i + 3; lane l lands at row 4 i + l / 16, physical
   // chunk l % 16, so it fetches the logical chunk that the swizzle puts there.
@@ -290,25 +358,25 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
     dma_off[i] = static_cast<uint32_t>(2 * (rip * a.c_s[2] + 8 * ((lane & 15) ^ tile_swizzle(rip))));
   }
   const char* const cache_bytes = static_cast<const char*>(a.cache);
+  // Byte strides of a block and of a 16-row group (32-bit: see prefill_supported).
+  const char* const cache_head = cache_bytes + 2 * head_elems;
+  const uint32_t blk_bytes = static_cast<uint32_t>(2 * a.c_s[1]);
+  const uint32_t grp_bytes = static_cast<uint32_t>(32 * a.c_s[2]);
 
   for (int32_t c0 = 0; c0 < ntiles; c0 += kChunkTiles) {
     const int32_t nt = ntiles - c0 < kChunkTiles ? ntiles - c0 : kChunkTiles;
     // Block ids of the chunk's pages; pages past the last visible key are
     // never looked up (their table entries may be anything).
     if (c0 > 0 || !hull_table) {
-      for (int i = tid; i < nt * 4; i += 256) {
-        const int32_t pos = base + kTileKeys * c0 + 16 * i;
-        page_tbl[i] = pos <= kmax ? static_cast<int32_t>(block_of(a, r, pos)) : -1;
-      }
+      for (int i = tid; i < nt; i += 256) fill_tile_record(page_tbl, a, r, i, base + kTileKeys * (c0 + i), kmax);
       __syncthreads();
     }
 
     // Wave w moves page w of each tile into LDS (K and V), four 1 KiB
-    // instructions each. Byte address of the K page segment of tile tl:
-    auto page_base = [&](int32_t tl, int32_t id) {
-      const uint32_t pos = static_cast<uint32_t>(base + kTileKeys * (c0 + tl) + 16 * wave);
-      const int64_t row0 = pos % bs32;
-      return cache_bytes + 2 * (static_cast<int64_t>(id) * a.c_s[1] + row0 * a.c_s[2] + head_elems);
+    // instructions each. Byte address of the K page segment with entry id:
+    auto page_base = [&](int32_t id) {
+      const uint32_t u = static_cast<uint32_t>(id);
+      return cache_head + static_cast<uint64_t>(u >> 4) * blk_bytes + (u & 15u) * grp_bytes;
     };
     // Unmapped page (or beyond the last visible key): its V rows are zeroed.
     auto zero_v = [&](int stage) {
@@ -331,29 +399,24 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
     // One tile: S = K . Q^T, softmax, O^T += V^T . P^T. LDS reads are issued
     // in batches ahead of the MFMAs that consume them (sched_barrier keeps
     // the compiler from sinking them next to their uses).
-    // The four block ids of a tile (one LDS read; tiles past the chunk read
-    // the last valid entry and are never used).
-    auto tile_ids = [&](int32_t tl) {
+    // This wave's record of a tile: its page's entry and the tile's
+    // valid-page mask (one LDS read; tiles past the chunk read the last
+    // valid record and are never used).
+    auto tile_rec = [&](int32_t tl) {
       const int32_t t = tl < nt ? tl : nt - 1;
-      return *reinterpret_cast<const int4*>(page_tbl + 4 * t);
+      return *reinterpret_cast<const int2*>(page_tbl + 8 * t + 2 * wave);
     };
-    auto page_mask = [&](int4 ids) {
-      return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-          (ids.x >= 0 ? 1 : 0) | (ids.y >= 0 ? 2 : 0) | (ids.z >= 0 ? 4 : 0) | (ids.w >= 0 ? 8 : 0)));
-    };
-    auto own_id = [&](int4 ids) {
-      const int32_t v = wave == 0 ? ids.x : wave == 1 ? ids.y : wave == 2 ? ids.z : ids.w;
-      return __builtin_amdgcn_readfirstlane(v);
-    };
+    auto own_id = [&](int2 rec) { return __builtin_amdgcn_readfirstlane(rec.x); };
+    auto page_mask = [&](int2 rec) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rec.y)); };
     // Wave-uniform page facts of tile tl (valid-page mask) and tile tl + 1
-    // (this wave's block id, mask), read from LDS one iteration ahead.
-    uint32_t cur_mask = page_mask(tile_ids(0));
+    // (this wave's page entry, mask), read from LDS one iteration ahead.
+    uint32_t cur_mask = page_mask(tile_rec(0));
     int32_t nxt_own;
     uint32_t nxt_mask;
     {
-      const int4 ids = tile_ids(1);
-      nxt_own = own_id(ids);
-      nxt_mask = page_mask(ids);
+      const int2 rec = tile_rec(1);
+      nxt_own = own_id(rec);
+      nxt_mask = page_mask(rec);
     }
     // The stage is a compile-time constant (the loop below is unrolled by
     // two), so LDS offsets fold into the instructions' offset fields.
@@ -363,18 +426,17 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
       // MFMAs below so that the address unit drains while the matrix cores
       // work (a burst of loads stalls the issuing wave).
       const int32_t nid = nxt_own;
-      // A load that is switched off (no next tile, or an unmapped page)
-      // still reads a mapped page but lands in the dummy region, so the
-      // sequence has no branches.
-      const bool dma_on = tl + 1 < nt && nid >= 0;
+      // The loads have no branches. An unmapped page still reads a mapped
+      // one: its K rows land in the other stage (its scores are masked), its
+      // V rows in the dummy region, as the stage's rows are being zeroed.
+      // With no next tile, nothing reads the other stage before the next
+      // chunk's first loads, which wait for these.
       if (tl + 1 < nt && nid < 0) zero_v(stage ^ 1);
-      const char* const kp = page_base(tl + 1, nid >= 0 ? nid : 0);
+      const char* const kp = page_base(nid >= 0 ? nid : 0);
       const char* const vp = kp + 2 * a.c_s[0];
-      const uint32_t kdst = dma_on ? kaddr + (stage ^ 1) * kTileBytes + wave * 4096 : daddr;
-      const uint32_t vdst = dma_on ? vaddr + (stage ^ 1) * kTileBytes + wave * 4096 : daddr;
-      const int4 fut_ids = tile_ids(tl + 2);
-      const uint8_t* kt = kbuf + stage * kTileBytes;
-      const uint8_t* vt = vbuf + stage * kTileBytes;
+      const uint32_t kdst = kaddr + (stage ^ 1) * kTileBytes + wave * 4096;
+      const uint32_t vdst = nid >= 0 ? vaddr + (stage ^ 1) * kTileBytes + wave * 4096 : daddr;
+      const int2 fut_rec = tile_rec(tl + 2);
 
       // Two halves of 32 keys, each a full online-softmax update.
 #pragma unroll
@@ -384,7 +446,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         const bool edge = k0 < w_lo_max || k0 + 31 > w_hi_min || pv != 3u;
         short8_t kf[8];
 #pragma unroll
-        for (int st = 0; st < 8; ++st) kf[st] = *reinterpret_cast<const short8_t*>(kt + 8192 * bb + koff[st]);
+        for (int st = 0; st < 8; ++st) kf[st] = lds_read_b128_at(klane[st] + stage * kTileBytes + 8192 * bb);
         __builtin_amdgcn_sched_barrier(0);
         float16v s_cur = float16v{};
 #pragma unroll
@@ -395,8 +457,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
             // during the second.
             const int i = st >> 1;
             __builtin_amdgcn_sched_barrier(0);
-            if (bb == 0) lds_dma_load16_sbase(kp, dma_off[i], kdst + (dma_on ? i * 1024 : 0));
-            else lds_dma_load16_sbase(vp, dma_off[i], vdst + (dma_on ? i * 1024 : 0));
+            page_load(bb == 0 ? kp : vp, i, dma_off[i], bb == 0 ? kdst : vdst);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -404,7 +465,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         // softmax (double-buffered: the second step is read during the first).
         short4v vf[2][8];
 #pragma unroll
-        for (int x = 0; x < 8; ++x) vf[0][x] = lds_read_tr16(vt + 8192 * bb + voff[x]);
+        for (int x = 0; x < 8; ++x) vf[0][x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb);
         __builtin_amdgcn_sched_barrier(0);
 
         // s_cur[i] = score of key k0 + 8 (i / 4) + 4 hh + i % 4, row n.
@@ -470,7 +531,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         for (int q = 0; q < 2; ++q) {
           if (q == 0) {
 #pragma unroll
-            for (int x = 0; x < 8; ++x) vf[1][x] = lds_read_tr16(vt + 8192 * bb + 256 * 16 + voff[x]);
+            for (int x = 0; x < 8; ++x) vf[1][x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb + 256 * 16);
           }
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
@@ -486,13 +547,13 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
       if (tl + 1 < nt) fix_v(tl + 1, stage ^ 1);
       __syncthreads();
       cur_mask = nxt_mask;
-      nxt_own = own_id(fut_ids);
-      nxt_mask = page_mask(fut_ids);
+      nxt_own = own_id(fut_rec);
+      nxt_mask = page_mask(fut_rec);
     };
 
     {
-      const int32_t id = own_id(tile_ids(0));
-      const char* kp = page_base(0, id >= 0 ? id : 0);
+      const int32_t id = own_id(tile_rec(0));
+      const char* kp = page_base(id >= 0 ? id : 0);
       if (id < 0) {
         zero_v(0);
       } else {
@@ -653,6 +714,10 @@ bool prefill_supported(const AttnArgs& a, int32_t dtype) {
   if (g != 1 && g != 2 && g != 4 && g != 8 && g != 16) return false;
   // Key positions and block ids are carried as int32 inside the kernel.
   if (a.width * a.block_size >= (int64_t{1} << 30) || a.num_blocks >= INT32_MAX) return false;
+  // Page-table entries pack (block id, 16-row group): 2^27 blocks of at most
+  // 256 rows; block and group strides fit 32-bit byte offsets.
+  if (a.num_blocks >= (int64_t{1} << 27) || a.block_size > 256) return false;
+  if (2 * a.c_s[1] >= (int64_t{1} << 32) || 32 * a.c_s[2] >= (int64_t{1} << 32)) return false;
   return true;
 }
 
