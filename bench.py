@@ -502,9 +502,11 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
     prefill_events = hip.create(2 * steps)
     stream = torch.cuda.current_stream(device).cuda_stream
     hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-    previous = os.environ.get("MVLLM_PREFILL_CONCURRENT")
+    saved = {k: os.environ.get(k) for k in ("MVLLM_PREFILL_CONCURRENT", "MVLLM_STEP_KERNEL")}
     if not concurrent:
+        # Separate launches on the caller's stream, warm-up steps included.
         os.environ["MVLLM_PREFILL_CONCURRENT"] = "0"
+        os.environ["MVLLM_STEP_KERNEL"] = "0"
 
     def step(i: int | None):
         timing = None
@@ -539,11 +541,11 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
                 # failed query leaves a HIP error behind: clear it.
                 hip.hip.hipGetLastError()
     finally:
-        if not concurrent:
-            if previous is None:
-                del os.environ["MVLLM_PREFILL_CONCURRENT"]
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
             else:
-                os.environ["MVLLM_PREFILL_CONCURRENT"] = previous
+                os.environ[k] = v
         hip.destroy(marks + decode_events + prefill_events)
     return out
 
