@@ -146,7 +146,8 @@ __device__ __forceinline__ short4v lds_read_tr16(const uint8_t* p) {
 }
 
 // lds_dma_load16_sbase with the LDS destination given as a wave-uniform
-// base plus an immediate, added straight into M0.
+// base plus an immediate, added straight into M0 (s_add_u32 also writes SCC,
+// which the clobber list declares).
 template <int OFF>
 __device__ __forceinline__ void lds_dma_load16_m0(const void* base, uint32_t offset, uint32_t lds_base) {
   asm volatile(
@@ -155,7 +156,7 @@ __device__ __forceinline__ void lds_dma_load16_m0(const void* base, uint32_t off
       "global_load_lds_dwordx4 %0, %2"
       :
       : "v"(offset), "s"(lds_base), "s"(base), "i"(OFF)
-      : "memory", "m0");
+      : "memory", "m0", "scc");
 }
 
 // Load i (of four) of a 16-row page: rows 4 i .. 4 i + 3, 1 KiB further into
