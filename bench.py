@@ -16,6 +16,9 @@ Reported (one JSON line on stdout):
   of 512 + 248 decodes): causal-visible FLOPs / its mean duration, against
   the 2.5 PFLOP/s bf16 peak (serial pass), and the mixed step's time with
   the decode and prefill workgroups in one step kernel;
+* ``kv_write``: the KV-cache write alone (one copy kernel) over the mixed
+  batch's tokens: K/V bytes read and written / its mean duration, against the
+  8 TB/s HBM peak (the shipped forward fuses the copy into its prologue);
 * ``e2e``: Qwen3-0.6B-shaped end-to-end output tok/s, synchronized steps
   summed (the reference's method) and, as ``value_pipelined``, with the host
   one graph step ahead;
@@ -482,6 +485,46 @@ def attention_workload(name: str, device):
     )
 
 
+def time_kv_write(w, hip: HipEvents, device, steps: int, warmup: int) -> dict:
+    """The KV-cache write on its own (``mvllm_kv_write``: one launch of
+    ``kv_write_rows_kernel``) over the batch's tokens, timed between HIP events
+    on the launch stream. The shipped forward fuses this copy into its
+    prologue launch; this is the copy kernel's own HBM rate."""
+
+    import torch
+
+    from micro_vllm_amd.attention.operators.mi355x_paged import hip_write_kv_cache
+
+    events = hip.create(2 * steps)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    for _ in range(warmup):
+        hip_write_kv_cache(w.key, w.value, w.cache, w.metadata)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        hip.hip.hipEventRecord(ctypes.c_void_p(events[2 * i]), ctypes.c_void_p(stream))
+        hip_write_kv_cache(w.key, w.value, w.cache, w.metadata)
+        hip.hip.hipEventRecord(ctypes.c_void_p(events[2 * i + 1]), ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    ms = statistics.mean(hip.elapsed_ms(events[2 * i], events[2 * i + 1]) for i in range(steps))
+    tokens = int(w.key.shape[0])
+    row_bytes = int(w.key.shape[1] * w.key.shape[2] * w.key.element_size())
+    moved = tokens * 2 * row_bytes * 2  # K and V rows, read and written
+    achieved = moved / (ms * 1e-3) / 1e9
+    return {
+        "kernel": "kv_write_rows_kernel",
+        "bound": "hbm",
+        "tokens": tokens,
+        "bytes": moved,
+        "kernel_us": round(ms * 1e3, 2),
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "note": "standalone copy; the shipped forward fuses it into the prologue launch",
+    }
+
+
 def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurrent: bool = True) -> dict:
     """``warmup`` untimed forwards, then ``steps`` timed ones between HIP
     events on the launch stream. ``concurrent`` True times the shipped step:
@@ -780,6 +823,9 @@ def main() -> int:
         record["mixed_step_ms_serial"] = round(serial["ms_per_step"], 5)
         record["decode_part_frac"] = round(decode_kernel_bytes(mixed) / (serial["decode_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         result["prefill"] = record
+        kv = time_kv_write(mixed, hip, device, args.steps, args.warmup)
+        kv["workload"] = f"llama3_mixed: the step's {kv['tokens']:,} tokens (8 KV heads, head_dim 128, bf16)"
+        result["kv_write"] = kv
         del mixed
         torch.cuda.empty_cache()
         run = run_generation(device, "qwen3_e2e", modes=("sync", "pipelined"))
