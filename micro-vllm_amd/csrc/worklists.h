@@ -49,12 +49,28 @@ inline int prefill_lg_tok(const AttnArgs& a) {
 // A slot < 0 or >= num_slots writes nothing.
 __device__ inline void copy_kv_row(const KvRowArgs& a, int64_t token, int first, int step) {
   const int64_t slot = a.slots[token];
+  const char* ksrc = a.key + token * a.key_token_stride;
+  const char* vsrc = a.value + token * a.value_token_stride;
+  if (first < 2 * a.chunks && first + step >= 2 * a.chunks) {
+    // One chunk per thread: its load does not depend on the slot, so it is
+    // issued before the slot is known and the two latencies overlap (a
+    // padding token's row exists too; only its store is skipped).
+    const bool is_value = first >= a.chunks;
+    const int chunk = is_value ? first - a.chunks : first;
+    const uint4 data = *reinterpret_cast<const uint4*>((is_value ? vsrc : ksrc) + 16 * chunk);
+    // Keep the slot's checks (and their wait) after the load is issued.
+    __builtin_amdgcn_sched_barrier(0);
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int64_t block = slot / a.block_size;
+    const int64_t offset = slot - block * a.block_size;
+    char* dst = a.cache + block * a.block_stride + offset * a.offset_stride;
+    *reinterpret_cast<uint4*>(dst + (is_value ? a.plane_stride : 0) + 16 * chunk) = data;
+    return;
+  }
   if (slot < 0 || slot >= a.num_slots) return;
   const int64_t block = slot / a.block_size;
   const int64_t offset = slot - block * a.block_size;
   char* dst = a.cache + block * a.block_stride + offset * a.offset_stride;
-  const char* ksrc = a.key + token * a.key_token_stride;
-  const char* vsrc = a.value + token * a.value_token_stride;
   for (int c = first; c < 2 * a.chunks; c += step) {
     const bool is_value = c >= a.chunks;
     const int chunk = is_value ? c - a.chunks : c;
