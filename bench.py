@@ -16,6 +16,9 @@ Reported (one JSON line on stdout):
   of 512 + 248 decodes): causal-visible FLOPs / its mean duration, against
   the 2.5 PFLOP/s bf16 peak (serial pass), and the mixed step's time with
   the decode and prefill workgroups in one step kernel;
+  ``prefill.library`` times the same chunks through PyTorch-ROCm's flash
+  attention (variable-length, one launch) and a square bf16 GEMM through
+  hipBLASLt on the same GPU;
 * ``kv_write``: the KV-cache write alone (one copy kernel) over the mixed
   batch's tokens: K/V bytes read and written / its mean duration, against the
   8 TB/s HBM peak (the shipped forward fuses the copy into its prologue);
@@ -29,7 +32,9 @@ Reported (one JSON line on stdout):
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload qwen3_decode] [--quick]
 
-Other workloads: ``llama3_mixed``, ``llama3_long_decode`` (attention steps),
+Other workloads: ``llama3_mixed``, ``llama3_long_decode``, ``llama3_long_prefill``
+(8 chunks of 512 at offsets U[14336, 16384]), ``llama3_causal_prefill`` (8
+causal chunks of 4,096 from position 0) (attention steps),
 ``qwen3_e2e`` and ``llama3_e2e`` (end-to-end generation; the Llama-3-8B one
 shares a 4,096-token prefix through the prefix cache and holds a ~200 GB KV
 cache).
@@ -54,6 +59,7 @@ for _p in (ROOT, ROOT / "micro-vllm_amd"):
 METRIC = "decode paged-attn HBM GB/s (% peak); e2e output tok/s, Qwen3-0.6B bf16"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+PREFILL_WORKLOADS = ("llama3_mixed", "llama3_long_prefill", "llama3_causal_prefill")
 
 
 class HipEvents:
@@ -332,6 +338,103 @@ def torch_baseline(w, reference_out, steps: int = 5, warmup: int = 2) -> dict:
     }
 
 
+def library_prefill_baseline(w, hip_out, steps: int = 10, warmup: int = 3) -> dict:
+    """The batch's prefill chunks through PyTorch-ROCm's flash attention on the
+    same GPU, and a square bf16 GEMM through ``torch.matmul`` (hipBLASLt) as the
+    library's own MFMA rate on this part, both timed between CUDA events on
+    torch's stream (medians).
+
+    The attention call is ``aten._flash_attention_forward`` in its
+    variable-length form: one launch over every chunk, each chunk's queries
+    against its whole context gathered into contiguous K/V (the gathers are
+    outside the timed region), causal with the mask aligned to the end of the
+    context (query i of a chunk of q tokens in a context of L sees keys
+    0..L-q+i, the paged kernels' rule), GQA by head grouping. Its output is
+    compared with the HIP path's."""
+
+    import math
+
+    import torch
+
+    from micro_vllm_amd import workloads
+
+    def median_ms(fn, warm: int) -> float:
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(steps):
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            fn()
+            stop.record()
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(stop))
+        return statistics.median(times)
+
+    out: dict = {}
+    n = 8192
+    a = torch.randn(n, n, device=w.query.device, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=w.query.device, dtype=torch.bfloat16)
+    # Twenty untimed products first: the part's clock settles under a long MFMA load.
+    ms = median_ms(lambda: torch.matmul(a, b), warm=20)
+    gemm_tflops = 2 * n**3 / (ms * 1e-3) / 1e12
+    out["gemm"] = {
+        "kind": f"torch.matmul {n}x{n}x{n} bf16 (hipBLASLt)",
+        "achieved": round(gemm_tflops, 1),
+        "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4),
+    }
+    del a, b
+
+    md = w.metadata
+    qsl = md.query_start_locations.tolist()
+    rows_q, keys, values = [], [], []
+    cum_q, cum_k = [0], [0]
+    for r, (length, q) in enumerate(zip(w.context_lengths.tolist(), w.query_lengths.tolist())):
+        if q <= 1:
+            continue
+        pos = torch.arange(length, device=w.query.device)
+        blocks = md.block_table[r, pos // w.block_size]
+        keys.append(w.cache[0, blocks, pos % w.block_size])
+        values.append(w.cache[1, blocks, pos % w.block_size])
+        rows_q.append((qsl[r], qsl[r + 1]))
+        cum_q.append(cum_q[-1] + q)
+        cum_k.append(cum_k[-1] + length)
+    query = torch.cat([w.query[s:e] for s, e in rows_q]).contiguous()
+    key = torch.cat(keys).contiguous()
+    value = torch.cat(values).contiguous()
+    del keys, values
+    cq = torch.tensor(cum_q, dtype=torch.int32, device=w.query.device)
+    ck = torch.tensor(cum_k, dtype=torch.int32, device=w.query.device)
+    max_q = max(e - s for s, e in rows_q)
+    max_k = max(cum_k[i + 1] - cum_k[i] for i in range(len(rows_q)))
+    scale = 1.0 / math.sqrt(w.head_dim)
+
+    def run():
+        return torch.ops.aten._flash_attention_forward(
+            query, key, value, cq, ck, max_q, max_k, 0.0, True, False, scale=scale
+        )[0]
+
+    try:
+        result = run()
+        ms = median_ms(run, warm=warmup)
+    except RuntimeError as exc:
+        out["flash_attention"] = {"unavailable": str(exc)[:160]}
+    else:
+        mine = torch.cat([hip_out[s:e] for s, e in rows_q]).float()
+        tflops = workloads.prefill_flops(w) / (ms * 1e-3) / 1e12
+        out["flash_attention"] = {
+            "kind": "torch aten._flash_attention_forward, variable-length, causal (end-aligned), GQA",
+            "us": round(ms * 1e3, 1),
+            "achieved": round(tflops, 1),
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "max_abs_diff_vs_hip": (result.float() - mine).abs().max().item(),
+        }
+    del query, key, value
+    torch.cuda.empty_cache()
+    return out
+
+
 def _subset_bytes(w, chosen) -> int:
     es = w.query.element_size()
     L = w.context_lengths[chosen]
@@ -473,6 +576,11 @@ def attention_workload(name: str, device):
         return workloads.llama3_long_decode(device), (
             "llama3_long_decode: 64 decode sequences, contexts U[8192,33280] seed 0, 32 q / 8 kv heads, "
             "head_dim 128, block 16, bf16, values N(0,1)"
+        )
+    if name == "llama3_causal_prefill":
+        return workloads.llama3_mixed(device, chunk_tokens=4096, offset_range=(0, 0), num_decodes=0), (
+            "llama3_causal_prefill: 8 prefill chunks x 4096 from position 0 (causal square, no decodes), "
+            "32 q / 8 kv heads, head_dim 128, block 16, bf16"
         )
     if name == "llama3_long_prefill":
         return workloads.llama3_mixed(device, offset_range=(14336, 16384), num_decodes=0), (
@@ -654,7 +762,15 @@ def main() -> int:
     parser.add_argument(
         "--workload",
         default="qwen3_decode",
-        choices=["qwen3_decode", "llama3_mixed", "llama3_long_prefill", "llama3_long_decode", "qwen3_e2e", "llama3_e2e"],
+        choices=[
+            "qwen3_decode",
+            "llama3_mixed",
+            "llama3_long_prefill",
+            "llama3_causal_prefill",
+            "llama3_long_decode",
+            "qwen3_e2e",
+            "llama3_e2e",
+        ],
     )
     parser.add_argument(
         "--quick",
@@ -729,7 +845,7 @@ def main() -> int:
     timing = time_attention(w, hip, device, args.steps, args.warmup)
     ms_per_step, decode_ms = timing["ms_per_step"], timing["decode_ms"]
     overlap = None
-    if args.workload in ("llama3_mixed", "llama3_long_prefill"):
+    if args.workload in PREFILL_WORKLOADS:
         # The library runs a mixed batch as one launch whose grid holds the
         # decode and the prefill workgroups. The step above is that shipped
         # one; each kernel's roofline comes from a second pass with the two
@@ -787,8 +903,13 @@ def main() -> int:
         result["control_plane"] = {"prefix_hash": measure_step_cost(w.context_lengths.tolist(), steps=3)}
     if overlap is not None:
         result["overlap"] = overlap
-    if args.workload in ("llama3_mixed", "llama3_long_prefill"):
+    if args.workload in PREFILL_WORKLOADS:
         result["prefill"] = prefill_record(w, serial)
+        from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
+
+        hip_out = hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata)
+        result["prefill"]["library"] = library_prefill_baseline(w, hip_out)
+        del hip_out
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=device)
@@ -822,6 +943,11 @@ def main() -> int:
         record["mixed_step_ms"] = round(shipped["ms_per_step"], 5)
         record["mixed_step_ms_serial"] = round(serial["ms_per_step"], 5)
         record["decode_part_frac"] = round(decode_kernel_bytes(mixed) / (serial["decode_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
+
+        mixed_out = hip_paged_attention(mixed.query, mixed.key, mixed.value, mixed.cache, mixed.metadata)
+        record["library"] = library_prefill_baseline(mixed, mixed_out)
+        del mixed_out
         result["prefill"] = record
         kv = time_kv_write(mixed, hip, device, args.steps, args.warmup)
         kv["workload"] = f"llama3_mixed: the step's {kv['tokens']:,} tokens (8 KV heads, head_dim 128, bf16)"
