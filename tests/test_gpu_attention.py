@@ -297,6 +297,44 @@ def test_prefill_kernel_bounded_specs(device, spec, hq, hkv):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
+@pytest.mark.parametrize(("hq", "hkv"), [(16, 8), (32, 8), (16, 16)], ids=["qwen3", "llama3", "mha"])
+def test_prefill_matches_platform_flash_attention(device, hq, hkv):
+    """An independent cross-check beside the oracle: the chunks' outputs
+    against PyTorch-ROCm's flash attention (``aten._flash_attention_forward``,
+    variable-length, causal with the mask aligned to the end of each
+    context, GQA by head grouping) over the same K/V, gathered from the
+    cache after the forward wrote the chunks' rows. Both compute in bf16
+    with fp32 accumulation."""
+
+    flash = getattr(torch.ops.aten, "_flash_attention_forward", None)
+    if flash is None:
+        pytest.skip("this torch build has no flash attention operator")
+    lengths = [700, 3000, 129, 600, 1100, 5000, 64]
+    qlens = [33, 512, 100, 600, 77, 130, 64]
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, hq, hkv, 128, 16, seed=hq + 5 * hkv)
+    out = operator()(q, k, v, cache, md)
+    torch.cuda.synchronize()
+    table, bs = md.block_table, md.block_size
+    keys, values = [], []
+    for r, length in enumerate(lengths):
+        pos = torch.arange(length, device=device)
+        blocks = table[r, pos // bs]
+        keys.append(cache[0, blocks, pos % bs])
+        values.append(cache[1, blocks, pos % bs])
+    cum_q = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=device)
+    cum_k = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32, device=device)
+    try:
+        ref = flash(
+            q.contiguous(), torch.cat(keys).contiguous(), torch.cat(values).contiguous(), cum_q, cum_k,
+            max(qlens), max(lengths), 0.0, True, False, scale=1.0 / math.sqrt(128),
+        )[0]
+    except RuntimeError as exc:
+        pytest.skip(f"flash attention is not available here: {exc}")
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
 def test_decode_work_list_beyond_65535_slots(device, monkeypatch):
     """One 16,384-token context beside 4,095 short ones: 1,024-token splits,
     17 per request, make 69,632 decode work-list slots (more than a 2-D grid
