@@ -215,6 +215,86 @@ void cross_wave_rates(float* out, unsigned long long* ticks, unsigned* simd, int
   std::printf("waves w and w + 4 on the same SIMD in every workgroup: %s\n", paired ? "yes" : "no");
 }
 
+// ------------------------------------- MFMA beside two vector ALU waves
+// Twelve waves per workgroup, one workgroup per CU: waves w, w + 4 and w + 8
+// share a SIMD. Waves 0-3 run back-to-back MFMAs (4 chains), waves 4-11 run
+// 16 independent chains of FMAs (or exponentials), each wave the same count.
+__global__ __launch_bounds__(768) void cross_wave3(float* out, unsigned long long* ticks, unsigned* simd, int mode,
+                                                  int iters) {
+  const int wave = threadIdx.x >> 6;
+  const int grp = wave >> 2;  // 0 MFMA, 1 and 2 vector ALU
+  const bool active = grp == 0 ? (mode & 1) : (mode & 2);
+  const unsigned id = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  float s = 0.f;
+  if (active && grp == 0) {
+    bf16x8 a, b;
+    operands(a, b);
+    float16v c[4];
+    for (int j = 0; j < 4; ++j) c[j] = float16v{};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c[j], 0, 0, 0);
+    }
+    for (int j = 0; j < 4; ++j) s += c[j][0];
+  } else if (active) {
+    float x[16];
+    for (int j = 0; j < 16; ++j) x[j] = 0.001f * ((threadIdx.x & 63) + j);
+    if (mode & 4) {
+      for (int it = 0; it < iters / 2; ++it) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) asm volatile("v_exp_f32_e64 %0, -%0" : "+v"(x[j]));
+      }
+    } else {
+      for (int it = 0; it < iters / 2; ++it) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) x[j] = __builtin_fmaf(x[j], 0.999f, 0.0001f);
+      }
+    }
+    for (int j = 0; j < 16; ++j) s += x[j];
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  sink(s, out);
+  if ((threadIdx.x & 63) == 0) {
+    ticks[blockIdx.x * 12 + wave] = t1 - t0;
+    simd[blockIdx.x * 12 + wave] = (id >> 4) & 3;
+  }
+}
+
+void cross_wave3_rates(float* out, unsigned long long* ticks, unsigned* simd, int cus) {
+  const int iters = 4000;
+  const size_t lds = 96 * 1024;  // one workgroup per CU
+  CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(cross_wave3), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)));
+  struct Mode {
+    int mode;
+    const char* name;
+  } modes[] = {{2, "fma"}, {3, "fma"}, {6, "exp"}, {7, "exp"}};
+  std::vector<unsigned long long> h(cus * 12);
+  std::vector<unsigned> hs(cus * 12);
+  bool paired = true;
+  for (const Mode& m : modes) {
+    hipLaunchKernelGGL(cross_wave3, dim3(cus), dim3(768), lds, 0, out, ticks, simd, m.mode, iters);
+    CHECK(hipGetLastError());
+    CHECK(hipDeviceSynchronize());
+    CHECK(hipMemcpy(h.data(), ticks, h.size() * 8, hipMemcpyDeviceToHost));
+    CHECK(hipMemcpy(hs.data(), simd, hs.size() * 4, hipMemcpyDeviceToHost));
+    std::vector<double> mf, span;
+    for (int b = 0; b < cus; ++b)
+      for (int w = 0; w < 4; ++w) {
+        mf.push_back(double(h[b * 12 + w]));
+        span.push_back(double(std::max(h[b * 12 + 4 + w], h[b * 12 + 8 + w])));
+        paired = paired && hs[b * 12 + w] == hs[b * 12 + 4 + w] && hs[b * 12 + w] == hs[b * 12 + 8 + w];
+      }
+    // Each vector wave issues 8 * iters instructions; both finish within the
+    // MFMA waves' run, so the later one's span bounds the pair's rate.
+    std::printf("one SIMD, two %s waves%-7s: %5.2f ticks per vector instruction between them%s", m.name,
+                (m.mode & 1) ? " + mfma" : "", median(span) / (2.0 * 8.0 * iters), (m.mode & 1) ? "" : "\n");
+    if (m.mode & 1) std::printf(", MFMA wave %6.2f ticks per MFMA\n", median(mf) / (iters * 4.0));
+  }
+  std::printf("waves w, w + 4 and w + 8 on the same SIMD in every workgroup: %s\n", paired ? "yes" : "no");
+}
+
 // ------------------------------------------ MFMA and VALU in the same wave
 // Each iteration: one MFMA (four chains in rotation) then K independent FMAs.
 template <int K>
@@ -516,6 +596,9 @@ int main() {
 
   std::printf("\n== MFMA and vector ALU work of two waves on one SIMD\n");
   cross_wave_rates(out, ticks, simd, cus);
+
+  std::printf("\n== MFMA beside two vector ALU waves on one SIMD\n");
+  cross_wave3_rates(out, ticks, simd, cus);
 
   std::printf("\n== MFMA and independent vector ALU work in one wave\n");
   in_wave_rate<0>(out, ticks, cus);
