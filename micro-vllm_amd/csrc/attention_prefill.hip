@@ -31,7 +31,10 @@
 // The online softmax (FlashAttention-2, Dao 2023) runs in the exp2 domain and
 // rescales the accumulators only when a row's maximum grows by more than 2^8
 // (lazy rescaling as in FlashAttention-3, Shah et al. 2024); the final
-// normalisation divides by a sum taken with the same offsets.
+// normalisation divides by a sum taken with the same offsets. In bf16, halves
+// that need no masking first skip the row maximum: their probabilities are
+// taken against the current offset, and the half is redone from its maximum
+// only if some lane's sum exceeds 2^12 (or is not finite).
 //
 // Masking: scores are masked only on tiles that cross a row's visible range
 // or hold an unmapped page. V rows outside the workgroup's visible key range
@@ -483,29 +486,34 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
             s_cur[i] = vis ? s_cur[i] : -INFINITY;
           }
         }
-        float mx = -INFINITY;
+        // Offset update from the half's row maximum: rescale when the
+        // maximum grew by more than 2^8 over the current offset.
+        auto rescale_to_max = [&]() {
+          float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[i]);
-        mx = max_with_partner(mx);
-        const float mx_c = mx * cs;
-        const bool grow = mx_c > m_c + 8.f;
-        if (__ballot(grow)) {
-          const float m_new = grow ? mx_c : m_c;
-          const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
-          l *= alpha;
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[i]);
+          mx = max_with_partner(mx);
+          const float mx_c = mx * cs;
+          const bool grow = mx_c > m_c + 8.f;
+          if (__ballot(grow)) {
+            const float m_new = grow ? mx_c : m_c;
+            const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
+            l *= alpha;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
-          m_c = m_new;
-        }
-        const float m_use = m_c == -INFINITY ? 0.f : m_c;
-
+            for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+            m_c = m_new;
+          }
+        };
         short8_t pb[2], pbl[2];
-        {
+        // Probabilities against offset m (P^T B operands in pb/pbl); returns
+        // this lane's share of their row sum (bf16: the rounded values).
+        auto make_p = [&](float m) {
+          float inc = 0.f;
           float p[16];
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[i], cs, -m_use));
-            if constexpr (PSPLIT) l += p[i];
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[i], cs, -m));
+            if constexpr (PSPLIT) inc += p[i];
           }
 #pragma unroll
           for (int s2 = 0; s2 < 2; ++s2) {
@@ -514,9 +522,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
               ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
-              // bf16: the row sum adds the rounded probabilities that the
-              // P.V product uses, two per instruction.
-              if constexpr (!PSPLIT) l = Mma32<T>::dot2_ones(ph[w], l);
+              if constexpr (!PSPLIT) inc = Mma32<T>::dot2_ones(ph[w], inc);
               if constexpr (PSPLIT) {
                 const float2v back = Mma32<T>::unpack2(ph[w]);
                 pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
@@ -525,7 +531,25 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
             pb[s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
             if constexpr (PSPLIT) pbl[s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
           }
+          return inc;
+        };
+        // Interior bf16 halves first try the current offset with no row
+        // maximum: a lane's 16 probabilities summing to at most 2^12 keep each
+        // below 2^12, which the accumulators hold; otherwise (a maximum that
+        // grew, an unset offset, NaN) the half is redone from its maximum.
+        float inc;
+        bool done = false;
+        if constexpr (!PSPLIT) {
+          if (!edge && !__ballot(m_c == -INFINITY)) {
+            inc = make_p(m_c);
+            done = !__ballot(!(inc <= 4096.f));
+          }
         }
+        if (!done) {
+          rescale_to_max();
+          inc = make_p(m_c == -INFINITY ? 0.f : m_c);
+        }
+        l += inc;
         __builtin_amdgcn_sched_barrier(0);
         // O^T += V^T . P^T over the half's two 16-key steps q.
 #pragma unroll
