@@ -297,6 +297,35 @@ def test_prefill_kernel_bounded_specs(device, spec, hq, hkv):
     run_and_check(q, k, v, cache, md, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_scores_that_jump_inside_unmasked_tiles(device, dtype):
+    """Scores that grow sharply at key positions inside tiles no row masks.
+    The bf16 kernel takes such tiles' probabilities against the running
+    offset without a row maximum and must notice the growth and redo them
+    (by 10, 14 and 150 powers of two over the first keys here), and both
+    dtypes must rescale their accumulators."""
+
+    lengths, qlens = [3000, 700], [64, 33]
+    hq, hkv, d, bs = 32, 8, 128, 16
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, hq, hkv, d, bs, seed=41)
+    gen = torch.Generator(device="cpu").manual_seed(41)
+    u = torch.randn(d, generator=gen)
+    u = (u / u.norm()).to(device)
+    scale_log2 = math.log2(math.e) / math.sqrt(d)
+    # Request 0's queries all point along u; its history keys gain a component
+    # along u that lifts their scores by 10, 14 and then 150 powers of two: a
+    # lane's 16 probabilities then sum to about 2^12, far above it, and past
+    # the fp32 range (2^128), where skipping the redo would give infinities.
+    q[:64] = (q[:64].float() * 0.1 + 8.0 * u).to(dtype)
+    table = md.block_table[0]
+    for lo, hi, lift in ((1024, 1536, 10.0), (1536, 2048, 14.0), (2048, 3000 - 64, 150.0)):
+        c = lift / scale_log2 / 8.0
+        pos = torch.arange(lo, hi, device=device)
+        blocks, rows = table[pos // bs], pos % bs
+        cache[0, blocks, rows] = (cache[0, blocks, rows].float() + c * u).to(dtype)
+    run_and_check(q, k, v, cache, md, dtype)
+
+
 @pytest.mark.parametrize(("hq", "hkv"), [(16, 8), (32, 8), (16, 16)], ids=["qwen3", "llama3", "mha"])
 def test_prefill_matches_platform_flash_attention(device, hq, hkv):
     """An independent cross-check beside the oracle: the chunks' outputs
