@@ -326,21 +326,22 @@ def test_prefill_scores_that_jump_inside_unmasked_tiles(device, dtype):
     run_and_check(q, k, v, cache, md, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize(("hq", "hkv"), [(16, 8), (32, 8), (16, 16)], ids=["qwen3", "llama3", "mha"])
-def test_prefill_matches_platform_flash_attention(device, hq, hkv):
+def test_prefill_matches_platform_flash_attention(device, hq, hkv, dtype):
     """An independent cross-check beside the oracle: the chunks' outputs
     against PyTorch-ROCm's flash attention (``aten._flash_attention_forward``,
     variable-length, causal with the mask aligned to the end of each
     context, GQA by head grouping) over the same K/V, gathered from the
-    cache after the forward wrote the chunks' rows. Both compute in bf16
-    with fp32 accumulation."""
+    cache after the forward wrote the chunks' rows. Both compute in the
+    input type with fp32 accumulation."""
 
     flash = getattr(torch.ops.aten, "_flash_attention_forward", None)
     if flash is None:
         pytest.skip("this torch build has no flash attention operator")
     lengths = [700, 3000, 129, 600, 1100, 5000, 64]
     qlens = [33, 512, 100, 600, 77, 130, 64]
-    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths, qlens, hq, hkv, 128, 16, seed=hq + 5 * hkv)
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, hq, hkv, 128, 16, seed=hq + 5 * hkv)
     out = operator()(q, k, v, cache, md)
     torch.cuda.synchronize()
     table, bs = md.block_table, md.block_size
@@ -361,7 +362,7 @@ def test_prefill_matches_platform_flash_attention(device, hq, hkv):
         pytest.skip(f"flash attention is not available here: {exc}")
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
-    torch.testing.assert_close(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(out.float(), ref.float(), **TOL[dtype])
 
 
 def test_decode_work_list_beyond_65535_slots(device, monkeypatch):
