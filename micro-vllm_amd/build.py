@@ -3,9 +3,7 @@
 Every ``csrc/*.hip`` file is compiled with ``hipcc --offload-arch=gfx950``
 into an object (in parallel), then linked into one shared library exposing
 the C ABI declared in ``include/mvllm_amd.h``. No torch extension machinery
-is involved: the library links only against the HIP runtime. The same run
-builds the hardware microbenchmarks (``probes/*.hip``), one executable each
-beside its source.
+is involved: the library links only against the HIP runtime.
 
     python micro-vllm_amd/build.py [--jobs N] [--verbose]
 """
@@ -23,7 +21,6 @@ from pathlib import Path
 PACKAGE_ROOT = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_ROOT.parent
 CSRC = PACKAGE_ROOT / "csrc"
-PROBES = PACKAGE_ROOT / "probes"
 INCLUDE = REPO_ROOT / "include"
 OBJ_DIR = PACKAGE_ROOT / "_build"
 LIB_DIR = PACKAGE_ROOT / "micro_vllm_amd" / "_lib"
@@ -69,34 +66,17 @@ def _compile(source: Path, verbose: bool) -> Path:
     return obj
 
 
-def _build_probe(source: Path, verbose: bool) -> Path:
-    exe = source.with_suffix("")
-    cmd = [hipcc(), *HIPCC_FLAGS, str(source), "-o", str(exe)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    result = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    stderr = "\n".join(line for line in result.stderr.splitlines() if noise not in line)
-    if result.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {source.name}:\n{stderr}")
-    return exe
-
-
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     """Compile every HIP source and link the shared library; return its path."""
 
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    probes = sorted(PROBES.glob("*.hip"))
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    workers = jobs or min(len(sources) + len(probes), max(1, min(8, os.cpu_count() or 1)))
+    workers = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        probe_jobs = [pool.submit(_build_probe, s, verbose) for s in probes]
         objects = list(pool.map(lambda s: _compile(s, verbose), sources))
-        for job in probe_jobs:
-            job.result()
     target = library_path()
     tmp = target.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
