@@ -25,6 +25,15 @@ Reported (one JSON line on stdout):
 * ``e2e``: Qwen3-0.6B-shaped end-to-end output tok/s, synchronized steps
   summed (the reference's method) and, as ``value_pipelined``, with the host
   one graph step ahead;
+* ``e2e_llama3``: Llama-3-8B-shaped end-to-end output tok/s (64 requests
+  sharing a 4,096-token prefix through the prefix cache, suffixes
+  U[4096, 28672], 512 greedy tokens each, ~200 GB KV cache), synchronized
+  steps summed, with the prefix-cache hit tokens and preemptions;
+* ``config1``: the reference's CPU-runnable case (contexts [17, 64, 130,
+  255]) through the HIP forward (fp32 and bf16) and the reference
+  operator's CPU path;
+* ``prefill.cpu_baseline``: the mixed batch's prefill chunks through the
+  reference operator's CPU path, in TFLOP/s;
 * ``gpu_baseline``: the same step in plain torch (block-table gather and
   matmuls) timed on the same GPU, and the HIP path's speedup over it;
 * ``cpu_baseline``: the reference operator's CPU path (torch, bf16 cache,
@@ -162,12 +171,13 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(w, sample_requests: int, repeats: int, warmups: int = 2) -> dict:
-    """Time the reference operator's CPU path (``oracle.reference_cpu``: the
-    steps of reference.py:14-138 in torch, bf16 cache, fp32 math) on this
-    host's cores, on ``sample_requests`` sequences of the batch (their blocks
-    copied into a compact host cache, the step's own K/V written by the
-    forward). Median of ``repeats`` runs after ``warmups``."""
+def cpu_forward_seconds(w, chosen, repeats: int, warmups: int = 2) -> tuple[float, int]:
+    """Median seconds of the reference operator's CPU path
+    (``oracle.reference_cpu``: the steps of reference.py:14-138 in torch,
+    the workload's cache dtype, fp32 math) over the requests ``chosen`` of
+    the batch, on every host core this process may use: their blocks are
+    copied into a compact host cache and the step's own K/V rows are written
+    by the forward. Returns (seconds, threads)."""
 
     import numpy as np
     import torch
@@ -178,9 +188,6 @@ def cpu_baseline(w, sample_requests: int, repeats: int, warmups: int = 2) -> dic
     previous = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        order = np.arange(len(w.context_lengths))
-        step = max(1, len(order) // sample_requests)
-        chosen = order[::step][:sample_requests]
         blocks = [w.block_lists[r] for r in chosen]
         ids = np.concatenate(blocks)
         compact = w.cache[:, torch.as_tensor(ids, device=w.cache.device)].cpu()
@@ -217,7 +224,20 @@ def cpu_baseline(w, sample_requests: int, repeats: int, warmups: int = 2) -> dic
         times = [run() for _ in range(repeats)]
     finally:
         torch.set_num_threads(previous)
-    seconds = statistics.median(times)
+    return statistics.median(times), threads
+
+
+def cpu_baseline(w, sample_requests: int, repeats: int, warmups: int = 2) -> dict:
+    """The reference operator's CPU path on ``sample_requests`` sequences of
+    a decode batch (evenly spaced), as HBM-equivalent GB/s: the same
+    algorithmic bytes the GPU step is credited with, over the CPU time."""
+
+    import numpy as np
+
+    order = np.arange(len(w.context_lengths))
+    step = max(1, len(order) // sample_requests)
+    chosen = order[::step][:sample_requests]
+    seconds, threads = cpu_forward_seconds(w, chosen, repeats, warmups)
     sample_bytes = _subset_bytes(w, chosen)
     return {
         "value": round(sample_bytes / seconds / 1e9, 4),
@@ -232,6 +252,82 @@ def cpu_baseline(w, sample_requests: int, repeats: int, warmups: int = 2) -> dic
             f"{seconds:.3f} s per forward"
         ),
     }
+
+
+def cpu_prefill_baseline(w, repeats: int = 3, warmups: int = 1) -> dict:
+    """The reference operator's CPU path on the batch's multi-query requests
+    (the prefill chunks), as TFLOP/s over the same causal-visible FLOPs the
+    GPU prefill kernel is credited with."""
+
+    import numpy as np
+
+    from micro_vllm_amd import workloads
+
+    chosen = np.nonzero(w.query_lengths > 1)[0]
+    seconds, threads = cpu_forward_seconds(w, chosen, repeats, warmups)
+    flops = workloads.prefill_flops(w)
+    return {
+        "value": round(flops / seconds / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "cpu_model": cpu_model(),
+        "sample": (
+            f"all {len(chosen)} prefill chunks ({int(w.query_lengths[chosen].sum())} queries, "
+            f"{flops / 1e9:.1f} GFLOP causal-visible) through the reference operator's CPU path "
+            f"(torch, {threads} threads, bf16 cache, fp32 math), median of {repeats} runs after {warmups}: "
+            f"{seconds:.3f} s per forward"
+        ),
+    }
+
+
+def small_mixed_record(hip: "HipEvents", device, steps: int = 200, warmup: int = 20) -> dict:
+    """The reference's CPU-runnable case on both sides: contexts
+    [17, 64, 130, 255] (a 17-token prefill and three decodes), 16 q / 8 KV
+    heads, head_dim 128, block 16, seed 0. The HIP forward is timed between
+    HIP events (mean over ``steps`` launches) in fp32 (the any-shape kernel)
+    and bf16 (the step kernel); the reference operator's CPU path in fp32 on
+    every host core (median of 7 runs after 3)."""
+
+    import numpy as np
+    import torch
+
+    from micro_vllm_amd import workloads
+    from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
+
+    hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    stream = torch.cuda.current_stream(device).cuda_stream
+    record = {
+        "workload": (
+            "small_mixed: contexts [17, 64, 130, 255] (one 17-token prefill + 3 decodes), 16 q / 8 kv heads, "
+            "head_dim 128, block 16, 64-block pool, seed 0"
+        )
+    }
+    for dtype, name in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        w = workloads.small_mixed(device, dtype=dtype)
+        events = hip.create(2)
+        for _ in range(warmup):
+            hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata)
+        torch.cuda.synchronize()
+        hip.hip.hipEventRecord(ctypes.c_void_p(events[0]), ctypes.c_void_p(stream))
+        for _ in range(steps):
+            hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata)
+        hip.hip.hipEventRecord(ctypes.c_void_p(events[1]), ctypes.c_void_p(stream))
+        torch.cuda.synchronize()
+        record[f"hip_us_{name}"] = round(hip.elapsed_ms(events[0], events[1]) * 1e3 / steps, 2)
+        hip.destroy(events)
+        if dtype == torch.float32:
+            seconds, threads = cpu_forward_seconds(w, np.arange(4), repeats=7, warmups=3)
+            record["cpu_baseline"] = {
+                "us": round(seconds * 1e6, 1),
+                "cores": threads,
+                "kind": "port",
+                "cpu_model": cpu_model(),
+                "sample": f"the whole batch through the reference operator's CPU path (torch, {threads} threads, fp32), "
+                "median of 7 runs after 3",
+            }
+    record["note"] = "latency-bound (20 query tokens); the HIP times include the forward's launches"
+    return record
 
 
 def torch_gathered_attention(query, key, value, cache, md, scale: float):
@@ -542,6 +638,15 @@ def run_generation(device, workload: str, *, modes=("sync",), requests: int | No
             "preemptions": result.preemptions,
             "prefix_hit_tokens": result.prefix_hit_tokens,
             "host_pack_ms_per_step": round(result.pack_seconds / max(result.steps, 1) * 1e3, 4),
+            # Synchronous decode steps on the engine's fast path, and their
+            # host phases per step: schedule (the step's arrays and blocks),
+            # pack (payload copy + pack launch), replay (graph launch and the
+            # tokens' copy issued), overlap (bookkeeping while the GPU runs),
+            # wait (until the step's tokens are on the host), append.
+            "fast_decode_steps": result.fast_decode_steps,
+            "fast_phase_ms": {
+                k: round(v / max(result.fast_decode_steps, 1) * 1e3, 4) for k, v in result.fast_phase_seconds.items()
+            },
             "output_tokens": result.output_tokens,
             "prompt_tokens": result.prompt_tokens,
         }
@@ -802,6 +907,9 @@ def main() -> int:
     parser.add_argument("--cpu-repeats", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument(
+        "--no-llama3-e2e", action="store_true", help="skip the Llama-3-8B end-to-end run of the default workload"
+    )
+    parser.add_argument(
         "--no-torch-baseline", action="store_true", help="skip the same-box torch gathered-attention baseline"
     )
     parser.add_argument(
@@ -905,6 +1013,8 @@ def main() -> int:
         result["overlap"] = overlap
     if args.workload in PREFILL_WORKLOADS:
         result["prefill"] = prefill_record(w, serial)
+        if not args.no_cpu_baseline:
+            result["prefill"]["cpu_baseline"] = cpu_prefill_baseline(w)
         from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
 
         hip_out = hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata)
@@ -931,10 +1041,12 @@ def main() -> int:
 
     if args.workload == "qwen3_decode" and not args.quick:
         # The other targets on their own configurations, in the same line:
-        # the prefill kernel on the Llama-3 mixed batch (bf16 MFMA roofline)
-        # and Qwen3-0.6B end-to-end output tok/s.
+        # the reference's CPU-runnable case on both sides, the prefill kernel
+        # on the Llama-3 mixed batch (bf16 MFMA roofline), Qwen3-0.6B and
+        # Llama-3-8B end-to-end output tok/s.
         del w
         torch.cuda.empty_cache()
+        result["config1"] = small_mixed_record(hip, device)
         mixed, mixed_description = attention_workload("llama3_mixed", device)
         shipped = time_attention(mixed, hip, device, args.steps, args.warmup)
         serial = time_attention(mixed, hip, device, args.steps, args.warmup, concurrent=False)
@@ -948,6 +1060,8 @@ def main() -> int:
         mixed_out = hip_paged_attention(mixed.query, mixed.key, mixed.value, mixed.cache, mixed.metadata)
         record["library"] = library_prefill_baseline(mixed, mixed_out)
         del mixed_out
+        if not args.no_cpu_baseline:
+            record["cpu_baseline"] = cpu_prefill_baseline(mixed)
         result["prefill"] = record
         kv = time_kv_write(mixed, hip, device, args.steps, args.warmup)
         kv["workload"] = f"llama3_mixed: the step's {kv['tokens']:,} tokens (8 KV heads, head_dim 128, bf16)"
@@ -965,6 +1079,21 @@ def main() -> int:
             "sync": sync,
             "pipelined": pipelined,
         }
+        del run
+        torch.cuda.empty_cache()
+        if not args.no_llama3_e2e:
+            run = run_generation(device, "llama3_e2e", modes=("sync",))
+            sync = run["modes"]["sync"]
+            result["e2e_llama3"] = {
+                "workload": run["workload"],
+                "parameters": run["parameters"],
+                "value": sync["output_tok_s"],
+                "unit": "output tok/s",
+                "timing": "synchronized engine steps summed (benchmarks/benchmark_engine.py:305-315)",
+                "sync": sync,
+            }
+            del run
+            torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
 

@@ -54,13 +54,19 @@ import weakref
 from collections import deque
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from micro_vllm_amd.attention.spec import FullAttentionSpec
 from micro_vllm_amd.harness.block_pool import BlockPool
 from micro_vllm_amd.harness.model import DecoderModel
 from micro_vllm_amd.harness.prefix_hash import BlockHashChain
-from micro_vllm_amd.worker.packing import DeviceBlockRows, allocate_packed_batch, pack_scheduler_output
+from micro_vllm_amd.worker.packing import (
+    DeviceBlockRows,
+    allocate_packed_batch,
+    pack_decode_rows,
+    pack_scheduler_output,
+)
 from micro_vllm_amd.worker.scheduler_output import (
     CacheGroupBlockTable,
     ScheduledRequest,
@@ -129,6 +135,12 @@ class GenerationResult:
     decode_seconds: float = 0.0
     prefix_hit_tokens: int = 0     # prompt tokens served by the prefix cache
     pack_seconds: float = 0.0      # host time spent packing steps (payload + launches)
+    # Decode steps taken by the fast path (synchronous mode): how many, and
+    # their host phases summed: schedule + pack + graph launch before the
+    # GPU runs, bookkeeping while it runs, the wait for its tokens, and the
+    # token appends after.
+    fast_decode_steps: int = 0
+    fast_phase_seconds: dict = field(default_factory=dict)
 
     @property
     def output_tokens_per_second(self) -> float:
@@ -188,6 +200,12 @@ class GenerationEngine:
         if pipeline and self.graphs is None:
             raise ValueError("pipeline=True needs decode_graphs=True")
         self.pipeline = pipeline
+        # Synchronous decode-only steps skip the plan objects (see
+        # _fast_decode_step); False forces every step through schedule().
+        self.fast_decode = True
+        self.fast_decode_steps = 0
+        self.fast_phase_seconds = {"schedule": 0.0, "pack": 0.0, "replay": 0.0, "overlap": 0.0, "wait": 0.0,
+                                   "append": 0.0}
 
     # ------------------------------------------------------------ requests
     def add_request(self, request: Request) -> None:
@@ -421,6 +439,13 @@ class GenerationEngine:
                 print(f"[generate] step {steps}, {done} output tokens, {len(self._running)} running", file=sys.stderr, flush=True)
                 next_report += progress_seconds
             start = time.perf_counter()
+            if pending is None and not self.pipeline and self._fast_decode_step():
+                elapsed = time.perf_counter() - start
+                seconds += elapsed
+                steps += 1
+                decode_steps += 1
+                decode_seconds += elapsed
+                continue
             plan = self.schedule()
             if self.pipeline and self.graphs.accepts(plan):
                 launched = self.graphs.launch(plan)
@@ -458,7 +483,119 @@ class GenerationEngine:
             decode_seconds=decode_seconds,
             prefix_hit_tokens=self.prefix_hit_tokens,
             pack_seconds=self.pack_seconds,
+            fast_decode_steps=self.fast_decode_steps,
+            fast_phase_seconds=dict(self.fast_phase_seconds),
         )
+
+    # ------------------------------------------------- decode fast path
+    def _fast_decode_step(self) -> bool:
+        """Run one decode-only graph step without building a plan, if the
+        scheduler's plan would be exactly that; return False (nothing
+        changed) otherwise.
+
+        The plan is "every running request, one token, sampled" when no
+        waiting request can be admitted (none waits, or every sequence slot
+        is taken), every running request is decode-ready (one known token
+        past its computed ones) and the pool holds every block the step needs
+        (no preemption). The step then does what schedule() + execute() +
+        _update() do, in the same order (blocks allocated in running order;
+        per request: count, prefix-cache commit, finish and free), with the
+        packing arrays built by numpy from the requests instead of one plan
+        object per request. The bookkeeping that does not need the sampled
+        tokens runs while the GPU computes them; the tokens are appended
+        after the step's device-to-host copy completes, so the step still
+        ends synchronized with its tokens on the host."""
+
+        g = self.graphs
+        running = self._running
+        n = len(running)
+        if (
+            not self.fast_decode
+            or g is None
+            or not self.incremental_block_table
+            or n == 0
+            or n > g.max_batch
+            or n > self.max_num_batched_tokens
+            or n > self.max_num_seqs
+            or (self._waiting and n < self.max_num_seqs)
+        ):
+            return False
+        t0 = time.perf_counter()
+        computed = np.fromiter((r.num_computed_tokens for r in running), np.int64, n)
+        known = np.fromiter((len(r.token_ids) for r in running), np.int64, n)
+        if not np.array_equal(known - computed, np.ones(n, np.int64)):
+            return False
+        bs = self.block_size
+        nblk = np.fromiter((len(r.block_ids) for r in running), np.int64, n)
+        short = np.nonzero(computed + 1 > nblk * bs)[0]
+        if len(short):
+            need = int(((computed[short] + bs) // bs - nblk[short]).sum())
+            if need > self.pool.num_free_blocks:
+                return False  # schedule() preempts
+            for i in short.tolist():
+                if not self._ensure_blocks(running[i], int(computed[i]) + 1):
+                    raise RuntimeError("block pool changed during a decode step")
+                nblk[i] = len(running[i].block_ids)
+        if self.block_rows is None:
+            self.block_rows = DeviceBlockRows(self.max_num_seqs, -(-self.max_model_len // bs), self.model.device)
+        rows = self.block_rows
+        slots = np.fromiter((rows.slot(r.request_id) for r in running), np.int64, n)
+        first = np.fromiter(
+            (r.row_sent if r.row_dirty is None else min(r.row_sent, r.row_dirty) for r in running), np.int64, n
+        )
+        updates = []
+        for i in np.nonzero(first < nblk)[0].tolist():
+            r, f, k = running[i], int(first[i]), int(nblk[i])
+            updates.append((int(slots[i]), f, r.block_ids[f:k]))
+            r.row_sent, r.row_dirty = k, None
+        tokens = np.fromiter((r.token_ids[-1] for r in running), np.int64, n)
+
+        size = g.bucket(n)
+        entry = g.entries.get(size) or g.capture(size)
+        t_pack = time.perf_counter()
+        with torch.inference_mode():
+            pack_decode_rows(
+                tokens, computed, nblk, slots, updates, spec=FullAttentionSpec(), block_size=bs,
+                null_block_id=self.null_block_id, block_rows=rows, into=entry.buffers,
+            )
+            t_replay = time.perf_counter()
+            self.pack_seconds += t_replay - t_pack
+            entry.graph.replay()
+            host = g._host[g._flip]
+            g._flip ^= 1
+            host[:n].copy_(entry.tokens[:n], non_blocking=True)
+            done = torch.cuda.Event()
+            done.record()
+        t1 = time.perf_counter()
+
+        # While the GPU runs: _update's per-request work that needs no token.
+        finished = []
+        for r in running:
+            r.num_computed_tokens += 1
+            if self.enable_prefix_cache:
+                self._commit(r)
+            if len(r.output_token_ids) + 1 >= r.max_tokens:
+                finished.append(r)
+                self._free(r)
+        if finished:
+            gone = set(map(id, finished))
+            self._running = [r for r in running if id(r) not in gone]
+        t2 = time.perf_counter()
+        done.synchronize()
+        t3 = time.perf_counter()
+        for r, token in zip(running, host[:n].tolist()):
+            r.output_token_ids.append(token)
+            r.token_ids.append(token)
+        t4 = time.perf_counter()
+        ph = self.fast_phase_seconds
+        ph["schedule"] += t_pack - t0
+        ph["pack"] += t_replay - t_pack
+        ph["replay"] += t1 - t_replay
+        ph["overlap"] += t2 - t1
+        ph["wait"] += t3 - t2
+        ph["append"] += t4 - t3
+        self.fast_decode_steps += 1
+        return True
 
     # ------------------------------------------------------- pipelining
     def _update_pending(self, plan: SchedulerOutput, step: "PendingStep") -> None:

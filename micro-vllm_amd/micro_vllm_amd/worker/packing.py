@@ -229,62 +229,30 @@ def pack_scheduler_output(
         hint = into.group_metadata[0].max_query_len
         if hint is not None and num_requests and int(scheduled.max()) > hint:
             raise ValueError(f"`into` is for steps of at most {hint} query tokens per request")
-    input_ids = into.input_ids
-    positions = into.positions
-    query_start_locations = into.group_metadata[0].query_start_locations
-    context_lengths = into.group_metadata[0].context_lengths
-    sampling_rows = into.sampling_row_indices
     lib = _native.load()
     stream = _native.stream_handle(device)
     base = payload.data_ptr()
     for g, spec in enumerate(specs):
         info_offset, ids_offset, total_blocks = group_layout[g]
-        group = into.group_metadata[g]
-        context_starts = group.query_context_start_positions
-        slot_mapping = group.slot_mapping
-        block_table = group.block_table
-        kind, parameter = spec.kernel_code()
-        first = g == 0
-        args = _native.PackArgs()
-        args.request_info = base + 4 * info_offset if num_requests else None
-        args.block_ids = base + 4 * ids_offset if total_blocks else None
-        args.token_ids = base if num_tokens else None
-        args.num_requests = num_requests
-        args.num_tokens = num_tokens
-        args.num_block_ids = total_blocks
-        args.block_size = block_size
-        args.null_block_id = null_block_id
-        args.spec_kind = kind
-        args.spec_parameter = parameter
-        args.token_capacity = token_capacity
-        args.request_capacity = request_capacity
-        args.block_table_width = widths[g]
-        args.input_ids = input_ids.data_ptr() if first and token_capacity else None
-        args.positions = positions.data_ptr() if first and token_capacity else None
-        args.context_starts = context_starts.data_ptr() if token_capacity else None
-        args.query_start_locations = query_start_locations.data_ptr() if first else None
-        args.context_lengths = context_lengths.data_ptr() if first and request_capacity else None
-        args.block_table = block_table.data_ptr() if block_table.numel() else None
-        args.slot_mapping = slot_mapping.data_ptr() if token_capacity else None
-        args.sampling_rows = sampling_rows.data_ptr() if first and num_sampling else None
+        args = _pack_args(
+            into, g, spec, base, info_offset=info_offset, ids_offset=ids_offset, total_blocks=total_blocks,
+            num_requests=num_requests, num_tokens=num_tokens, num_sampling=num_sampling, block_size=block_size,
+            null_block_id=null_block_id, token_capacity=token_capacity, request_capacity=request_capacity,
+            width=widths[g],
+        )
         if block_rows is None:
             _native.check(lib.mvllm_pack_batch(args, stream), "mvllm_pack_batch")
         else:
-            rows = _native.BlockRows()
-            rows.rows = block_rows.rows.data_ptr()
-            rows.num_slots = block_rows.num_slots
-            rows.width = block_rows.width
-            rows.updates = base + 4 * updates_offset if len(row_updates) else None
-            rows.num_updates = len(row_updates)
+            rows = _rows_args(block_rows, base, updates_offset, len(row_updates))
             _native.check(lib.mvllm_pack_batch_rows(args, rows, stream), "mvllm_pack_batch_rows")
     # `payload` was allocated on the current stream, so the caching allocator
     # reuses its memory only for work ordered after these launches.
     return PackedBatch(
-        input_ids=input_ids,
-        positions=positions,
+        input_ids=into.input_ids,
+        positions=into.positions,
         group_metadata=into.group_metadata,
         request_ids=tuple(r.request_id for r in requests),
-        sampling_row_indices=sampling_rows[:num_sampling],
+        sampling_row_indices=into.sampling_row_indices[:num_sampling],
     )
 
 
@@ -324,4 +292,120 @@ def allocate_packed_batch(
         group_metadata=metadata,
         request_ids=(),
         sampling_row_indices=torch.empty(sampling_capacity, **i64),
+    )
+
+
+def _pack_args(into: PackedBatch, g: int, spec: AttentionSpec, base: int, *, info_offset: int, ids_offset: int,
+               total_blocks: int, num_requests: int, num_tokens: int, num_sampling: int, block_size: int,
+               null_block_id: int, token_capacity: int, request_capacity: int, width: int) -> "_native.PackArgs":
+    """The C arguments of one cache group's pack launch: payload sections
+    at the given int32 offsets from ``base``, outputs into ``into``."""
+
+    group = into.group_metadata[g]
+    kind, parameter = spec.kernel_code()
+    first = g == 0
+    args = _native.PackArgs()
+    args.request_info = base + 4 * info_offset if num_requests else None
+    args.block_ids = base + 4 * ids_offset if total_blocks else None
+    args.token_ids = base if num_tokens else None
+    args.num_requests = num_requests
+    args.num_tokens = num_tokens
+    args.num_block_ids = total_blocks
+    args.block_size = block_size
+    args.null_block_id = null_block_id
+    args.spec_kind = kind
+    args.spec_parameter = parameter
+    args.token_capacity = token_capacity
+    args.request_capacity = request_capacity
+    args.block_table_width = width
+    args.input_ids = into.input_ids.data_ptr() if first and token_capacity else None
+    args.positions = into.positions.data_ptr() if first and token_capacity else None
+    args.context_starts = group.query_context_start_positions.data_ptr() if token_capacity else None
+    args.query_start_locations = group.query_start_locations.data_ptr() if first else None
+    args.context_lengths = group.context_lengths.data_ptr() if first and request_capacity else None
+    args.block_table = group.block_table.data_ptr() if group.block_table.numel() else None
+    args.slot_mapping = group.slot_mapping.data_ptr() if token_capacity else None
+    args.sampling_rows = into.sampling_row_indices.data_ptr() if first and num_sampling else None
+    return args
+
+
+def _rows_args(block_rows: DeviceBlockRows, base: int, updates_offset: int, num_updates: int) -> "_native.BlockRows":
+    rows = _native.BlockRows()
+    rows.rows = block_rows.rows.data_ptr()
+    rows.num_slots = block_rows.num_slots
+    rows.width = block_rows.width
+    rows.updates = base + 4 * updates_offset if num_updates else None
+    rows.num_updates = num_updates
+    return rows
+
+
+def pack_decode_rows(
+    token_ids: np.ndarray,
+    computed: np.ndarray,
+    block_lengths: np.ndarray,
+    slots: np.ndarray,
+    row_updates: Sequence[tuple[int, int, Sequence[int]]],
+    *,
+    spec: AttentionSpec,
+    block_size: int,
+    null_block_id: int,
+    block_rows: DeviceBlockRows,
+    into: PackedBatch,
+) -> PackedBatch:
+    """Pack a decode-only step (every request: one token, sampled) from
+    per-request arrays, without a ``SchedulerOutput``: the same launch and
+    outputs as ``pack_scheduler_output(plan, into=into, block_rows=...,
+    row_updates=...)`` for the plan whose request r has input token
+    ``token_ids[r]``, ``computed[r]`` computed tokens and
+    ``block_lengths[r]`` block ids in block row ``slots[r]``.
+    ``row_updates`` lists ``(slot, first, ids)``: the ids that changed in a
+    row since it was last written."""
+
+    device = into.input_ids.device
+    n = int(len(token_ids))
+    token_capacity = into.input_ids.numel()
+    request_capacity = into.group_metadata[0].context_lengths.numel()
+    width = into.group_metadata[0].block_table.shape[1]
+    if n > token_capacity or n > request_capacity or into.sampling_row_indices.numel() < n:
+        raise ValueError(f"a decode step of {n} requests exceeds the buffers' capacities")
+    if n and int(block_lengths.max()) > min(width, block_rows.width):
+        raise ValueError("a block list is longer than the block table")
+    counts = [len(u[2]) for u in row_updates]
+    total_blocks = sum(counts)
+    info = np.zeros((n, _native.PACK_FIELDS), dtype=np.int32)
+    info[:, 0] = computed
+    info[:, 1] = 1
+    info[:, 2] = block_lengths
+    info[:, 3] = 1
+    info[:, 6] = slots
+    records = np.zeros((len(row_updates), 4), dtype=np.int32)
+    ids_offset = 0
+    for i, ((slot, first, _), k) in enumerate(zip(row_updates, counts)):
+        if first < 0 or first + k > block_rows.width:
+            raise ValueError(f"row update of slot {slot} exceeds the block rows' width")
+        records[i] = (slot, first, k, ids_offset)
+        ids_offset += k
+    ids = np.fromiter(chain.from_iterable(u[2] for u in row_updates), dtype=np.int32, count=total_blocks)
+    host = torch.from_numpy(np.concatenate((np.asarray(token_ids, np.int32), info.reshape(-1), ids, records.reshape(-1))))
+    if host.numel() == 0:
+        host = torch.zeros(1, dtype=torch.int32)
+    payload = host.pin_memory().to(device, non_blocking=True)
+    base = payload.data_ptr()
+    info_offset = n
+    ids_at = n + info.size
+    updates_offset = ids_at + total_blocks
+    args = _pack_args(
+        into, 0, spec, base, info_offset=info_offset, ids_offset=ids_at, total_blocks=total_blocks, num_requests=n,
+        num_tokens=n, num_sampling=n, block_size=block_size, null_block_id=null_block_id,
+        token_capacity=token_capacity, request_capacity=request_capacity, width=width,
+    )
+    rows = _rows_args(block_rows, base, updates_offset, len(row_updates))
+    lib = _native.load()
+    _native.check(lib.mvllm_pack_batch_rows(args, rows, _native.stream_handle(device)), "mvllm_pack_batch_rows")
+    return PackedBatch(
+        input_ids=into.input_ids,
+        positions=into.positions,
+        group_metadata=into.group_metadata,
+        request_ids=(),
+        sampling_row_indices=into.sampling_row_indices[:n],
     )

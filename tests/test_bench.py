@@ -121,3 +121,17 @@ def test_cpu_baseline_runs_the_reference_cpu_path_on_every_host_thread():
     assert r["cores"] == bench.host_threads() >= 1
     assert "4 of 4 sequences" in r["sample"] and r["cpu_model"]
     assert torch.equal(w.cache, before)  # the baseline works on a host copy
+
+
+def test_cpu_prefill_baseline_times_only_the_prefill_chunks():
+    import torch
+
+    sys.path.insert(0, str(ROOT / "micro-vllm_amd"))
+    from micro_vllm_amd import workloads
+
+    w = workloads.small_mixed("cpu", dtype=torch.bfloat16)
+    r = bench.cpu_prefill_baseline(w, repeats=2, warmups=1)
+    assert r["kind"] == "port" and r["unit"] == "TFLOP/s" and r["value"] > 0
+    assert "all 1 prefill chunks (17 queries" in r["sample"]
+    # 17 causal queries from position 0: 17 * 18 / 2 visible pairs, 4 * Hq * D flops each.
+    assert f"{4 * 16 * 128 * 153 / 1e9:.1f} GFLOP" in r["sample"]

@@ -25,7 +25,9 @@ from _golden import GOLDEN, batch_from_case, cache_from_case
 from _oracle_bridge import (
     assert_attention_close,
     assert_cache_bit_exact,
+    forward_checking_write,
     oracle_step,
+    sampled_rows_step,
     subset_step,
     to_oracle,
 )
@@ -593,12 +595,12 @@ def check_whole_batch(w, out, group=32):
 
 def test_llama3_mixed_batch_whole(device):
     """The Llama-3-head mixed batch (8 chunks of 512 at offsets U[0, 2048] +
-    248 decodes U[256, 8192], 4,344 tokens): every request against the
-    oracle."""
+    248 decodes U[256, 8192], 4,344 tokens) through the shipped forward (one
+    step kernel, K/V written in its prologue): the whole cache bit-exact
+    after the write, every request against the oracle."""
 
     w = workloads.llama3_mixed(device)
-    out = operator()(w.query, w.key, w.value, w.cache, w.metadata)
-    torch.cuda.synchronize()
+    out = forward_checking_write(operator(), w.query, w.key, w.value, w.cache, w.metadata)
     check_whole_batch(w, out)
 
 
@@ -612,11 +614,11 @@ def test_small_mixed_batch(device, dtype):
 
 def test_qwen3_decode_batch_whole(device):
     """The 256-sequence Qwen3 decode batch (contexts U[128, 4096], 70k-block
-    pool): every request against the oracle."""
+    pool) through the shipped forward: the whole 4.6 GB cache bit-exact after
+    the write, every request against the oracle."""
 
     w = workloads.qwen3_decode(device)
-    out = operator()(w.query, w.key, w.value, w.cache, w.metadata)
-    torch.cuda.synchronize()
+    out = forward_checking_write(operator(), w.query, w.key, w.value, w.cache, w.metadata)
     check_whole_batch(w, out, group=64)
 
 
@@ -706,6 +708,43 @@ def test_shared_4096_token_prefix_suffix_prefill_and_decode(device, hq, hkv):
     out = run_and_check(q, k, v, cache, md, torch.bfloat16)
     assert torch.equal(cache[:, shared].view(torch.int16), prefix_before.view(torch.int16))
     assert torch.equal(out[:512], out[512:1024])
+
+
+@pytest.mark.parametrize("hint", ["max", None], ids=["hint", "no-hint"])
+def test_llama3_heads_at_long_context_positions(device, hint):
+    """The Llama-3-8B end-to-end configuration's attention shapes at its own
+    positions: 32/8 heads; a 4,096-token prefix held once in shared blocks
+    (prefix cache, kv_cache_manager.py:113-134); suffix prefill chunks of 512
+    and 704 queries at offsets 24,096 and 28,196 (after the prefix and a
+    suffix history); decodes at contexts 30,097, 32,997 and 33,280 (the
+    longest prefix + suffix + output, 4,096 + 28,672 + 512). The whole
+    cache is checked bit-exact after the write (the prefix blocks
+    untouched); 120 sampled query rows (chunk edges, 32-row and 128-row
+    boundaries, random rows, every decode) are checked against the oracle
+    over their full visible ranges."""
+
+    plan = [(20_000, 512), (28_900, 1), (24_100, 704), (26_000, 1), (29_183, 1)]
+    q, k, v, cache, md, shared = shared_prefix_case(device, 4096, plan, 32, 8, seed=63)
+    if hint is None:
+        md = dataclasses.replace(md, max_query_len=None)
+    assert int(md.context_lengths.max()) == 33_280
+    prefix_before = cache[:, shared].clone()
+    out = forward_checking_write(operator(), q, k, v, cache, md)
+    assert torch.equal(cache[:, shared].view(torch.int16), prefix_before.view(torch.int16))
+    assert not torch.isnan(out).any()
+    qsl = md.query_start_locations.cpu().tolist()
+    rng = np.random.default_rng(63)
+    rows = []
+    for r, (_, n) in enumerate(plan):
+        first = qsl[r]
+        if n == 1:
+            rows.append(first)
+            continue
+        edges = [0, 1, 31, 32, 63, 64, 127, 128, 255, 256, n - 2, n - 1]
+        rows.extend(first + e for e in edges)
+        rows.extend(first + int(x) for x in rng.choice(n, size=40, replace=False))
+    rows, expected = sampled_rows_step(q, cache, md, rows)
+    assert_attention_close(out[torch.as_tensor(rows, device=device)], expected, **TOL[torch.bfloat16])
 
 
 @pytest.mark.parametrize("step_kernel", ["2", "0"])

@@ -79,29 +79,35 @@ def teacher_forced_logits(model, sequences, device, last=None):
     return model.logits(hidden).float()
 
 
-def check_against_reference(requests, hip_model, ref_model, device):
+def check_against_reference(requests, hip_model, ref_model, device, group=None):
     """Teacher-forced check of every generated position (see module doc):
-    identical greedy tokens, on a margin the test verifies."""
+    identical greedy tokens, on a margin the test verifies. ``group`` bounds
+    how many sequences are teacher-forced in one step."""
 
-    sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in requests]
-    last = [len(r.output_token_ids) for r in requests]
-    ref_logits = teacher_forced_logits(ref_model, sequences, device, last)
-    hip_logits = teacher_forced_logits(hip_model, sequences, device, last)
-    assert torch.isfinite(hip_logits).all()
-    max_diff = (hip_logits - ref_logits).abs().max().item()
-
-    offset, checked, min_gap, divergence = 0, 0, float("inf"), None
-    for r, k in zip(requests, last):
-        rows = ref_logits[offset : offset + k]
-        offset += k
-        top2 = rows.topk(2, dim=-1)
-        expected = top2.indices[:, 0].tolist()
-        gap = (top2.values[:, 0] - top2.values[:, 1]).tolist()
-        for i, (got, want, g) in enumerate(zip(r.output_token_ids, expected, gap)):
-            checked += 1
-            min_gap = min(min_gap, g)
-            if got != want and divergence is None:
-                divergence = (r.request_id, i, got, want, g)
+    group = group or len(requests)
+    max_diff = 0.0
+    checked, min_gap, divergence = 0, float("inf"), None
+    for g0 in range(0, len(requests), group):
+        part = requests[g0 : g0 + group]
+        sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in part]
+        last = [len(r.output_token_ids) for r in part]
+        ref_logits = teacher_forced_logits(ref_model, sequences, device, last)
+        hip_logits = teacher_forced_logits(hip_model, sequences, device, last)
+        assert torch.isfinite(hip_logits).all()
+        max_diff = max(max_diff, (hip_logits - ref_logits).abs().max().item())
+        offset = 0
+        for r, k in zip(part, last):
+            rows = ref_logits[offset : offset + k]
+            offset += k
+            top2 = rows.topk(2, dim=-1)
+            expected = top2.indices[:, 0].tolist()
+            gap = (top2.values[:, 0] - top2.values[:, 1]).tolist()
+            for i, (got, want, g) in enumerate(zip(r.output_token_ids, expected, gap)):
+                checked += 1
+                min_gap = min(min_gap, g)
+                if got != want and divergence is None:
+                    divergence = (r.request_id, i, got, want, g)
+        del ref_logits, hip_logits
     print(f"{checked} positions; max |logit difference| {max_diff:.4f}; smallest reference top-2 gap {min_gap:.3f}")
     if divergence is not None:
         print("first divergence: request %s output %d: got %d, reference %d (reference gap %.4f)" % divergence)
@@ -225,6 +231,38 @@ def test_pipelined_decode_with_preemption_matches_synchronous_decode(device):
     assert outputs[0] == outputs[1]
 
 
+@pytest.mark.parametrize("prefix_cache", [False, True], ids=["plain", "prefix-cache"])
+def test_fast_decode_steps_match_the_planned_steps(device, prefix_cache):
+    """Synchronous decode-only steps taken by the engine's fast path (arrays
+    instead of plan objects, token-independent bookkeeping while the GPU
+    runs) against the same engine with every step planned by schedule():
+    identical tokens, the same steps, and the same block pool afterwards
+    (free list order, reference counts, prefix-cache index). The requests
+    cross block boundaries, finish at different steps, arrive while others
+    decode, and one round runs short of blocks (preemption: the fast path
+    must hand such steps to schedule())."""
+
+    hip_model, _ = models(device, seed=13, fused_layers=True)
+    runs = []
+    for fast in (False, True):
+        requests = make_requests(seed=13, count=10, lo=20, hi=90, max_tokens=30)
+        for i, r in enumerate(requests):
+            r.max_tokens = 20 + 4 * i
+        engine = GenerationEngine(
+            hip_model, num_blocks=30, max_num_batched_tokens=128, max_num_seqs=6, max_model_len=256,
+            decode_graphs=True, enable_prefix_cache=prefix_cache,
+        )
+        engine.fast_decode = fast
+        result = engine.generate(requests)
+        pool = engine.pool
+        runs.append((result.outputs, result.steps, result.decode_steps, result.preemptions,
+                     list(pool._free), list(pool._ref), dict(pool._index), result.fast_decode_steps))
+    slow, fast = runs
+    assert fast[7] > 10 and slow[7] == 0
+    assert slow[3] > 0  # preemption happened
+    assert fast[:7] == slow[:7]
+
+
 def test_decode_graph_replays_match_eager_on_the_same_buffers(device):
     """Every replay of a captured decode step equals an eager forward on the
     same static buffers, bit for bit, with eager work between replays."""
@@ -283,6 +321,41 @@ def test_qwen3_0_6b_shape_greedy_tokens_match_reference(device):
     result = engine.generate(requests)
     assert result.output_tokens == 12 * 32
     assert check_against_reference(requests, hip_model, ref_model, device) == 12 * 32
+
+
+def test_qwen3_0_6b_config_scheduler_greedy_tokens_match_reference(device):
+    """The end-to-end Qwen3-0.6B configuration's model AND scheduler settings:
+    28 layers, hidden 1024, 16/8 heads of 128, qk-norm, MLP 3072, vocab
+    151,936; 256 requests with prompts U[64, 1024]; max_num_batched_tokens
+    8,192 and max_num_seqs 256, so prefill steps pack many prompts and mix
+    with decodes; HIP-graph decode steps with the host one step ahead. Output
+    lengths U[16, 40] make the running set shrink, so the decode graphs of
+    buckets 256, 128 and 64 (and the smaller ones) are all replayed. Every
+    one of the ~7,000 generated tokens must equal the reference-semantics
+    operator's teacher-forced greedy choice."""
+
+    hip_model, ref_model = models(device, seed=23, fused_layers=True, num_hidden_layers=28, vocab_size=QWEN3_VOCAB)
+    requests = make_requests(seed=23, count=256, lo=64, hi=1024, max_tokens=16, vocab=QWEN3_VOCAB)
+    rng = np.random.default_rng(24)
+    for r in requests:
+        r.max_tokens = int(rng.integers(16, 41))
+    engine = GenerationEngine(
+        hip_model,
+        num_blocks=256 * 67 + 1,
+        max_num_batched_tokens=8192,
+        max_num_seqs=256,
+        max_model_len=67 * 16,
+        decode_graphs=True,
+        pipeline=True,
+    )
+    result = engine.generate(requests)
+    expected_tokens = sum(r.max_tokens for r in requests)
+    assert result.output_tokens == expected_tokens
+    assert {64, 128, 256} <= set(engine.graphs.entries), sorted(engine.graphs.entries)
+    assert result.decode_steps >= 16
+    del engine
+    torch.cuda.empty_cache()
+    assert check_against_reference(requests, hip_model, ref_model, device, group=32) == expected_tokens
 
 
 def test_random_init_logits_agree_at_qwen3_0_6b_shape(device):

@@ -236,3 +236,60 @@ def test_device_block_rows_give_the_oracle_packing_over_steps(device):
             torch.cuda.synchronize()
             check_against_oracle(packed, requests, [FullAttentionSpec()], block_size=16, null_block_id=null, capacities=caps)
             updates = []  # the rows already hold them for the padded pass
+
+
+def test_decode_rows_packing_equals_the_plan_packing(device):
+    """``pack_decode_rows`` (a decode-only step packed from per-request
+    arrays, the engine's fast path) writes exactly what
+    ``pack_scheduler_output`` writes for the same decode plan: every buffer
+    of a graph bucket bit-identical, with row updates (new rows, appended
+    ids, a replaced entry) applied to the device-resident table the same
+    way, over several steps."""
+
+    from micro_vllm_amd.worker.packing import DeviceBlockRows, allocate_packed_batch, pack_decode_rows
+
+    rng = np.random.default_rng(31)
+    null, width, cap = 4999, 40, 16
+    rows_a = DeviceBlockRows(num_slots=cap, width=width, device=device)
+    rows_b = DeviceBlockRows(num_slots=cap, width=width, device=device)
+    bufs = [allocate_packed_batch(num_groups=1, block_size=16, token_capacity=cap, request_capacity=cap,
+                                  block_table_widths=[width], sampling_capacity=cap, device=device, max_query_len=1)
+            for _ in range(2)]
+    reqs = {f"r{i}": dict(ids=rng.permutation(4000)[: int(rng.integers(1, 30))].tolist(), sent=0) for i in range(11)}
+    for step in range(4):
+        if step == 2:
+            reqs["r3"]["ids"][1] = 4100      # prefix-cache switch to a canonical block
+            reqs["r3"]["sent"] = 1
+        if step == 3:
+            reqs["r5"]["ids"].append(4200)  # a new block
+        names = list(reqs)
+        computed = np.array([len(reqs[k]["ids"]) * 16 - int(rng.integers(1, 16)) for k in names], np.int64)
+        tokens = rng.integers(0, 50_000, size=len(names)).astype(np.int64)
+        updates = [(k, reqs[k]["sent"], reqs[k]["ids"][reqs[k]["sent"]:]) for k in names
+                   if reqs[k]["sent"] < len(reqs[k]["ids"])]
+        for k in names:
+            reqs[k]["sent"] = len(reqs[k]["ids"])
+        items = [
+            ScheduledRequest(k, (int(t),), int(c), 1, True, (CacheGroupBlockTable(tuple(reqs[k]["ids"])),))
+            for k, t, c in zip(names, tokens, computed)
+        ]
+        a = pack_scheduler_output(SchedulerOutput(tuple(items)), specs=[FullAttentionSpec()], block_size=16,
+                                  null_block_id=null, device=device, into=bufs[0], block_rows=rows_a,
+                                  row_updates=updates)
+        slots = np.array([rows_b.slot(k) for k in names], np.int64)
+        b = pack_decode_rows(
+            tokens, computed, np.array([len(reqs[k]["ids"]) for k in names], np.int64), slots,
+            [(rows_b.slot(k), f, ids) for k, f, ids in updates], spec=FullAttentionSpec(), block_size=16,
+            null_block_id=null, block_rows=rows_b, into=bufs[1],
+        )
+        torch.cuda.synchronize()
+        assert torch.equal(rows_a.rows, rows_b.rows)
+        for x, y in ((a.input_ids, b.input_ids), (a.positions, b.positions),
+                     (a.sampling_row_indices, b.sampling_row_indices)):
+            assert torch.equal(x, y)
+        ma, mb = a.group_metadata[0], b.group_metadata[0]
+        for f in ("query_context_start_positions", "query_start_locations", "context_lengths", "block_table",
+                  "slot_mapping"):
+            assert torch.equal(getattr(ma, f), getattr(mb, f)), (step, f)
+        assert b.input_ids[: len(names)].tolist() == tokens.tolist()
+
