@@ -41,6 +41,10 @@ struct AttnArgs {
   int64_t num_tokens, num_requests, num_blocks, block_size;
   int32_t num_q_heads, num_kv_heads, group, head_dim;
   float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
+  // log2(block_size / 16) when block_size is a multiple of 16 whose
+  // quotient is a power of two (16-key pages are then found with shifts),
+  // else -1.
+  int32_t page_shift = -1;
   // Split-KV decode partials: acc [R][max_splits][Hq][D], (max, sum) [R][max_splits][Hq].
   float* ws_acc;
   float2* ws_ml;

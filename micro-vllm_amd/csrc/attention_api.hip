@@ -238,6 +238,11 @@ void fill_batch_args(AttnArgs& a, const mvllm_batch* batch, const mvllm_kv_cache
   a.num_requests = batch->num_requests;
   a.num_blocks = cache->num_blocks;
   a.block_size = cache->block_size;
+  a.page_shift = -1;
+  if (cache->block_size >= 16 && cache->block_size % 16 == 0) {
+    const int64_t pages = cache->block_size / 16;
+    if ((pages & (pages - 1)) == 0) a.page_shift = __builtin_ctzll(static_cast<unsigned long long>(pages));
+  }
   a.num_q_heads = static_cast<int32_t>(Hq);
   a.num_kv_heads = static_cast<int32_t>(cache->num_kv_heads);
   a.group = static_cast<int32_t>(Hq / cache->num_kv_heads);

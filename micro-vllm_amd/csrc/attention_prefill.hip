@@ -183,7 +183,15 @@ __device__ __forceinline__ short4v lds_read_tr16_at(uint32_t addr) {
 
 // Page-table entry of the 16-key page at position pos: (block id << 4) |
 // (the page's 16-row group inside its block), or -1 for an unmapped page.
-__device__ __forceinline__ int32_t page_entry(const AttnArgs& a, int64_t r, int64_t pos) {
+// `row` is the request's block-table row. With a power-of-two number of
+// pages per block the block and group come from shifts of pos / 16 (32-bit:
+// positions stay below 2^30); otherwise from 64-bit division.
+__device__ __forceinline__ int32_t page_entry(const AttnArgs& a, const int64_t* row, int64_t r, int32_t pos) {
+  if (a.page_shift >= 0) {
+    const uint32_t p16 = static_cast<uint32_t>(pos) >> 4;
+    const int64_t b = row[static_cast<int64_t>(p16 >> a.page_shift) * a.t_s1];
+    return (b >= 0 && b < a.num_blocks) ? static_cast<int32_t>((b << 4) | (p16 & ((1u << a.page_shift) - 1u))) : -1;
+  }
   const int64_t b = block_of(a, r, pos);
   return b >= 0 ? static_cast<int32_t>((b << 4) | ((pos % a.block_size) >> 4)) : -1;
 }
@@ -193,12 +201,13 @@ __device__ __forceinline__ int32_t page_entry(const AttnArgs& a, int64_t r, int6
 // (-1 past `last` or unmapped) and the tile's valid-page mask.
 __device__ __forceinline__ void fill_tile_record(int32_t* tbl, const AttnArgs& a, int64_t r, int i, int32_t tpos,
                                                  int32_t last) {
+  const int64_t* row = a.table + r * a.t_s0;
   int32_t e[4];
   uint32_t mask = 0;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const int32_t pos = tpos + 16 * w;
-    e[w] = pos <= last ? page_entry(a, r, pos) : -1;
+    e[w] = pos <= last ? page_entry(a, row, r, pos) : -1;
     mask |= e[w] >= 0 ? 1u << w : 0u;
   }
   int4* rec = reinterpret_cast<int4*>(tbl + 8 * i);
@@ -277,15 +286,27 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
     red[2 * wave + 1] = w_hi_max;
   }
 
-  // Q^T as B operands: lane (n, hh) holds row n, dims 16 st + 8 hh .. +8.
+  // Q^T as B operands: lane (n, hh) holds row n, dims 16 st + 8 hh .. +8,
+  // each multiplied by the softmax scale in the exp2 domain (log2(e) /
+  // sqrt(D)) and rounded back to the input type, so the MFMAs produce
+  // scaled scores and the softmax needs no multiply.
   short8_t qv[8];
   {
     const short8_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
     const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (row_ok ? tok : t0) * a.q_s0 +
                          static_cast<int64_t>(hq) * a.q_s1 + 8 * hh;
 #pragma unroll
-    for (int st = 0; st < 8; ++st)
-      qv[st] = row_ok ? *reinterpret_cast<const short8_t*>(qp + 16 * st) : zero;
+    for (int st = 0; st < 8; ++st) {
+      const short8_t raw = row_ok ? *reinterpret_cast<const short8_t*>(qp + 16 * st) : zero;
+      const uint4 w = __builtin_bit_cast(uint4, raw);
+      uint32_t sw[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float2v f = Mma32<T>::unpack2(sw[j]);
+        sw[j] = Mma32<T>::pack2(f[0] * a.scale_log2, f[1] * a.scale_log2);
+      }
+      qv[st] = __builtin_bit_cast(short8_t, uint4{sw[0], sw[1], sw[2], sw[3]});
+    }
   }
   __syncthreads();
   int32_t kmin = INT_MAX, kmax = -1;
@@ -308,9 +329,15 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
   float16v oacc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) oacc[c] = float16v{};
-  float m_c = -INFINITY;  // running offset of this row (exp2 domain)
+  // Softmax state of this lane's row, in the exp2 domain. m_c is the
+  // running offset (-inf until the row has seen a visible key); the S MFMAs
+  // start from the accumulator value -c_in, so they produce scores already
+  // shifted by c_in = (m_c finite ? m_c : 0), and halves whose offset does
+  // not change take exp2 of the MFMA results directly.
+  float m_c = -INFINITY;
+  float c_in = 0.f;
+  float16v neg_c = float16v{};
   float l = 0.f;          // this lane's share of the row's softmax sum
-  const float cs = a.scale_log2;
 
   const int64_t head_elems = static_cast<int64_t>(h) * kDim;
   const int32_t base = kmax >= kmin ? (kmin & ~15) : 0;
@@ -452,7 +479,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
 #pragma unroll
         for (int st = 0; st < 8; ++st) kf[st] = lds_read_b128_at(klane[st] + stage * kTileBytes + 8192 * bb);
         __builtin_amdgcn_sched_barrier(0);
-        float16v s_cur = float16v{};
+        float16v s_cur = neg_c;
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
           s_cur = Mma32<T>::mma(kf[st], qv[st], s_cur);
@@ -472,7 +499,8 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         for (int x = 0; x < 8; ++x) vf[0][x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb);
         __builtin_amdgcn_sched_barrier(0);
 
-        // s_cur[i] = score of key k0 + 8 (i / 4) + 4 hh + i % 4, row n.
+        // s_cur[i] = scaled score of key k0 + 8 (i / 4) + 4 hh + i % 4, row
+        // n, minus c_in.
         if (edge) {
           // The empty asm keeps the compiler from if-converting the masking
           // into every step: interior steps skip it entirely.
@@ -493,7 +521,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
 #pragma unroll
           for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[i]);
           mx = max_with_partner(mx);
-          const float mx_c = mx * cs;
+          const float mx_c = mx + c_in;
           const bool grow = mx_c > m_c + 8.f;
           if (__ballot(grow)) {
             const float m_new = grow ? mx_c : m_c;
@@ -505,14 +533,16 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
           }
         };
         short8_t pb[2], pbl[2];
-        // Probabilities against offset m (P^T B operands in pb/pbl); returns
-        // this lane's share of their row sum (bf16: the rounded values).
-        auto make_p = [&](float m) {
+        // Probabilities exp2(s_cur + shift) (P^T B operands in pb/pbl), the
+        // add skipped for SHIFTED false; returns this lane's share of their
+        // row sum (bf16: the rounded values).
+        auto make_p = [&](float shift, auto shifted_c) {
+          constexpr bool SHIFTED = decltype(shifted_c)::value;
           float inc = 0.f;
           float p[16];
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[i], cs, -m));
+            p[i] = __builtin_amdgcn_exp2f(SHIFTED ? s_cur[i] + shift : s_cur[i]);
             if constexpr (PSPLIT) inc += p[i];
           }
 #pragma unroll
@@ -533,21 +563,25 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
           }
           return inc;
         };
-        // Interior bf16 halves first try the current offset with no row
-        // maximum: a lane's 16 probabilities summing to at most 2^12 keep each
-        // below 2^12, which the accumulators hold; otherwise (a maximum that
-        // grew, an unset offset, NaN) the half is redone from its maximum.
+        // bf16 halves first try the current offset with no row maximum (the
+        // scores already carry it): a lane's 16 probabilities summing to at
+        // most 2^12 keep each below 2^12, which the accumulators hold;
+        // otherwise (a maximum that grew, an unset offset, NaN) the half is
+        // redone from its maximum and the offset moves.
         float inc;
         bool done = false;
         if constexpr (!PSPLIT) {
-          if (!edge && !__ballot(m_c == -INFINITY)) {
-            inc = make_p(m_c);
+          if (!__ballot(m_c == -INFINITY)) {
+            inc = make_p(0.f, std::false_type{});
             done = !__ballot(!(inc <= 4096.f));
           }
         }
         if (!done) {
           rescale_to_max();
-          inc = make_p(m_c == -INFINITY ? 0.f : m_c);
+          const float m_eff = m_c == -INFINITY ? 0.f : m_c;
+          inc = make_p(c_in - m_eff, std::true_type{});
+          c_in = m_eff;
+          neg_c = float16v{} - m_eff;
         }
         l += inc;
         __builtin_amdgcn_sched_barrier(0);
