@@ -469,129 +469,67 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
       const uint32_t vdst = nid >= 0 ? vaddr + (stage ^ 1) * kTileBytes + wave * 4096 : daddr;
       const int2 fut_rec = tile_rec(tl + 2);
 
-      // Two halves of 32 keys, each a full online-softmax update.
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        const int32_t k0 = base + kTileKeys * (c0 + tl) + 32 * bb;
-        const uint32_t pv = (cur_mask >> (2 * bb)) & 3u;
-        const bool edge = k0 < w_lo_max || k0 + 31 > w_hi_min || pv != 3u;
-        short8_t kf[8];
+      // The tile as two halves of 32 keys, each a full online-softmax
+      // update, ordered so that each half's softmax runs beside MFMAs of the
+      // same wave: S(0); softmax(0) beside S(1); softmax(1) beside P.V(0);
+      // P.V(1). Each pairing is one basic block on the common path, so the
+      // compiler interleaves the vector and matrix instructions.
+      auto half_k0 = [&](int bb) { return base + kTileKeys * (c0 + tl) + 32 * bb; };
+      auto half_pages = [&](int bb) { return (cur_mask >> (2 * bb)) & 3u; };
+      auto half_edge = [&](int bb) {
+        const int32_t k0 = half_k0(bb);
+        return k0 < w_lo_max || k0 + 31 > w_hi_min || half_pages(bb) != 3u;
+      };
+      auto read_k = [&](int bb, short8_t (&kf)[8]) {
 #pragma unroll
         for (int st = 0; st < 8; ++st) kf[st] = lds_read_b128_at(klane[st] + stage * kTileBytes + 8192 * bb);
-        __builtin_amdgcn_sched_barrier(0);
-        float16v s_cur = neg_c;
+      };
+      // V operands of both 16-key steps of half bb (transposing reads).
+      auto read_v = [&](int bb, short4v (&vf)[2][8]) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int x = 0; x < 8; ++x) vf[q][x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb + 4096 * q);
+      };
+      // S^T of half bb from the K fragments, starting at `init` (-c_in), with
+      // the loads of tile tl + 1 between the MFMAs: K pages with half 0, V
+      // pages with half 1. PIN places each load after its MFMA pair.
+      auto s_chain = [&](int bb, const short8_t (&kf)[8], float16v init, auto pin_c) {
+        constexpr bool PIN = decltype(pin_c)::value;
+        float16v s = init;
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
-          s_cur = Mma32<T>::mma(kf[st], qv[st], s_cur);
+          s = Mma32<T>::mma(kf[st], qv[st], s);
           if (st & 1) {
-            // Loads of tile tl + 1: K pages during the first half, V pages
-            // during the second.
             const int i = st >> 1;
-            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (PIN) __builtin_amdgcn_sched_barrier(0);
             page_load(bb == 0 ? kp : vp, i, dma_off[i], bb == 0 ? kdst : vdst);
-            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (PIN) __builtin_amdgcn_sched_barrier(0);
           }
         }
-        // V operands of the half's first 16-key step, in flight during the
-        // softmax (double-buffered: the second step is read during the first).
-        short4v vf[2][8];
+        return s;
+      };
+      // s[i] = scaled score of key k0 + 8 (i / 4) + 4 hh + i % 4, row n,
+      // minus c_in: -inf outside the row's visible range or on an unmapped
+      // page.
+      auto mask = [&](int bb, float16v& s) {
+        const int32_t k0 = half_k0(bb);
+        const uint32_t pv = half_pages(bb);
+        // kk = 8 (i / 4) + 4 hh + i % 4: the lane's 4 hh goes into the
+        // bounds, so each compare takes an immediate.
+        const int32_t rlo = lo_n - k0 - 4 * hh, rhi = hi_n - k0 - 4 * hh;
 #pragma unroll
-        for (int x = 0; x < 8; ++x) vf[0][x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb);
-        __builtin_amdgcn_sched_barrier(0);
-
-        // s_cur[i] = scaled score of key k0 + 8 (i / 4) + 4 hh + i % 4, row
-        // n, minus c_in.
-        if (edge) {
-          // The empty asm keeps the compiler from if-converting the masking
-          // into every step: interior steps skip it entirely.
-          asm volatile("");
-          const int32_t rlo = lo_n - k0, rhi = hi_n - k0;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kk = 8 * (i >> 2) + 4 * hh + (i & 3);
-            const bool page_ok = (pv >> (i >> 3)) & 1u;
-            const bool vis = page_ok && kk >= rlo && kk <= rhi;
-            s_cur[i] = vis ? s_cur[i] : -INFINITY;
-          }
+        for (int i = 0; i < 16; ++i) {
+          constexpr int kk_base[16] = {0, 1, 2, 3, 8, 9, 10, 11, 16, 17, 18, 19, 24, 25, 26, 27};
+          const bool page_ok = (pv >> (i >> 3)) & 1u;
+          const bool vis = page_ok && kk_base[i] >= rlo && kk_base[i] <= rhi;
+          s[i] = vis ? s[i] : -INFINITY;
         }
-        // Offset update from the half's row maximum: rescale when the
-        // maximum grew by more than 2^8 over the current offset.
-        auto rescale_to_max = [&]() {
-          float mx = -INFINITY;
+      };
+      // O^T += V^T . P^T over a half's two 16-key steps.
+      auto pv_mma = [&](const short4v (&vf)[2][8], const short8_t (&pb)[2], const short8_t (&pbl)[2]) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[i]);
-          mx = max_with_partner(mx);
-          const float mx_c = mx + c_in;
-          const bool grow = mx_c > m_c + 8.f;
-          if (__ballot(grow)) {
-            const float m_new = grow ? mx_c : m_c;
-            const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
-            l *= alpha;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
-            m_c = m_new;
-          }
-        };
-        short8_t pb[2], pbl[2];
-        // Probabilities exp2(s_cur + shift) (P^T B operands in pb/pbl), the
-        // add skipped for SHIFTED false; returns this lane's share of their
-        // row sum (bf16: the rounded values).
-        auto make_p = [&](float shift, auto shifted_c) {
-          constexpr bool SHIFTED = decltype(shifted_c)::value;
-          float inc = 0.f;
-          float p[16];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(SHIFTED ? s_cur[i] + shift : s_cur[i]);
-            if constexpr (PSPLIT) inc += p[i];
-          }
-#pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2) {
-            // P^T B operand: keys 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
-            uint32_t ph[4], pl[4];
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
-              if constexpr (!PSPLIT) inc = Mma32<T>::dot2_ones(ph[w], inc);
-              if constexpr (PSPLIT) {
-                const float2v back = Mma32<T>::unpack2(ph[w]);
-                pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
-              }
-            }
-            pb[s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
-            if constexpr (PSPLIT) pbl[s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
-          }
-          return inc;
-        };
-        // bf16 halves first try the current offset with no row maximum (the
-        // scores already carry it): a lane's 16 probabilities summing to at
-        // most 2^12 keep each below 2^12, which the accumulators hold;
-        // otherwise (a maximum that grew, an unset offset, NaN) the half is
-        // redone from its maximum and the offset moves.
-        float inc;
-        bool done = false;
-        if constexpr (!PSPLIT) {
-          if (!__ballot(m_c == -INFINITY)) {
-            inc = make_p(0.f, std::false_type{});
-            done = !__ballot(!(inc <= 4096.f));
-          }
-        }
-        if (!done) {
-          rescale_to_max();
-          const float m_eff = m_c == -INFINITY ? 0.f : m_c;
-          inc = make_p(c_in - m_eff, std::true_type{});
-          c_in = m_eff;
-          neg_c = float16v{} - m_eff;
-        }
-        l += inc;
-        __builtin_amdgcn_sched_barrier(0);
-        // O^T += V^T . P^T over the half's two 16-key steps q.
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          if (q == 0) {
-#pragma unroll
-            for (int x = 0; x < 8; ++x) vf[1][x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb + 256 * 16);
-          }
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             const short4v lo4 = vf[q][c], hi4 = vf[q][4 + c];
@@ -599,9 +537,126 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
             oacc[c] = Mma32<T>::mma(av, pb[q], oacc[c]);
             if constexpr (PSPLIT) oacc[c] = Mma32<T>::mma(av, pbl[q], oacc[c]);
           }
-          __builtin_amdgcn_sched_barrier(0);
+      };
+      // Probabilities exp2(s + shift) (P^T B operands in pb/pbl), the add
+      // skipped for SHIFTED false; returns this lane's share of their row
+      // sum (bf16: the rounded values).
+      auto make_p = [&](const float16v& s, float shift, auto shifted_c, short8_t (&pb)[2], short8_t (&pbl)[2]) {
+        constexpr bool SHIFTED = decltype(shifted_c)::value;
+        float inc = 0.f;
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          p[i] = __builtin_amdgcn_exp2f(SHIFTED ? s[i] + shift : s[i]);
+          if constexpr (PSPLIT) inc += p[i];
         }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          // P^T B operand: keys 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
+          uint32_t ph[4], pl[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
+            if constexpr (!PSPLIT) inc = Mma32<T>::dot2_ones(ph[w], inc);
+            if constexpr (PSPLIT) {
+              const float2v back = Mma32<T>::unpack2(ph[w]);
+              pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
+            }
+          }
+          pb[s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
+          if constexpr (PSPLIT) pbl[s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
+        }
+        return inc;
+      };
+      // From the half's row maximum: a new offset when the maximum grew by
+      // more than 2^8 over the current one (the accumulators and the sum
+      // rescaled), then the probabilities against it; c_in follows.
+      auto softmax_slow = [&](float16v& s, short8_t (&pb)[2], short8_t (&pbl)[2]) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        mx = max_with_partner(mx);
+        const float mx_c = mx + c_in;
+        const bool grow = mx_c > m_c + 8.f;
+        if (__ballot(grow)) {
+          const float m_new = grow ? mx_c : m_c;
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_c - m_new) : 1.f;
+          l *= alpha;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) oacc[c] *= alpha;
+          m_c = m_new;
+        }
+        const float m_eff = m_c == -INFINITY ? 0.f : m_c;
+        const float inc = make_p(s, c_in - m_eff, std::true_type{}, pb, pbl);
+        c_in = m_eff;
+        neg_c = float16v{} - m_eff;
+        return inc;
+      };
+      // A half's softmax with `work` (MFMAs of this wave that do not depend
+      // on it) in the same block. bf16 halves first try the current offset
+      // with no row maximum (the scores already carry it): a lane's 16
+      // probabilities summing to at most 2^12 keep each below 2^12, which
+      // the accumulators hold; otherwise (a maximum that grew, an unset
+      // offset, NaN) the half is redone from its maximum.
+      auto softmax_with = [&](float16v& s, short8_t (&pb)[2], short8_t (&pbl)[2], auto&& work) {
+        float inc = 0.f;
+        bool done = false;
+        work();
+        if constexpr (!PSPLIT) {
+          // Speculative: the probabilities are formed in the same block as
+          // `work`, and kept only when every lane has an offset.
+          inc = make_p(s, 0.f, std::false_type{}, pb, pbl);
+          done = !__ballot(m_c == -INFINITY || !(inc <= 4096.f));
+        }
+        if (!done) inc = softmax_slow(s, pb, pbl);
+        return inc;
+      };
+
+      // V operands of one 16-key step of half bb.
+      auto read_v1 = [&](int bb, int q, short4v (&vq)[8]) {
+#pragma unroll
+        for (int x = 0; x < 8; ++x) vq[x] = lds_read_tr16_at(vlane[x] + stage * kTileBytes + 8192 * bb + 4096 * q);
+      };
+      short4v vf[2][8];
+      float16v s0, s1;
+      {
+        short8_t kf[8];
+        read_k(0, kf);
+        __builtin_amdgcn_sched_barrier(0);
+        s0 = s_chain(0, kf, neg_c, std::true_type{});
       }
+      read_v1(0, 0, vf[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (half_edge(0)) {
+        // The empty asm keeps the compiler from if-converting the masking
+        // into every tile: interior halves skip it entirely.
+        asm volatile("");
+        mask(0, s0);
+      }
+      short8_t pb0[2], pbl0[2];
+      l += softmax_with(s0, pb0, pbl0, [] {});
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        short8_t kf[8];
+        read_k(1, kf);
+        __builtin_amdgcn_sched_barrier(0);
+        s1 = s_chain(1, kf, neg_c, std::true_type{});
+      }
+      read_v1(0, 1, vf[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (half_edge(1)) {
+        asm volatile("");
+        mask(1, s1);
+      }
+      // softmax(1) beside P.V(0).
+      short8_t pb1[2], pbl1[2];
+      l += softmax_with(s1, pb1, pbl1, [&] { pv_mma(vf, pb0, pbl0); });
+      __builtin_amdgcn_sched_barrier(0);
+      read_v1(1, 0, vf[0]);
+      read_v1(1, 1, vf[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      pv_mma(vf, pb1, pbl1);
+      __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt<0>();
       if (tl + 1 < nt) fix_v(tl + 1, stage ^ 1);
       __syncthreads();
