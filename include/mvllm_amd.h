@@ -204,7 +204,10 @@ int mvllm_attention_forward(const mvllm_tensor3* query,
  * counterpart in the reference. The workspace is a library-owned device
  * array of MVLLM_NOALLOC_SCRATCH_BYTES per device (its address is looked up
  * once per device on the first call there); the call allocates nothing and
- * runs all of its work on `stream` (no side stream). A batch that needs more
+ * runs all of its work on `stream` (no side stream). Graph capture: make the
+ * first call on a device outside capture; a first call under capture is
+ * refused with MVLLM_ERR_INVALID (the address lookup may load code), later
+ * calls capture and replay like mvllm_attention_forward. A batch that needs more
  * workspace (mvllm_attention_workspace_bytes) is rejected with
  * MVLLM_ERR_WORKSPACE. Every call on one device shares that array: calls
  * that overlap on one device (other streams, other threads) race and give

@@ -463,6 +463,9 @@ namespace {
 
 // Device address of `scratch` on the device that `stream` belongs to,
 // looked up on the first call for that device (with it current) and kept.
+// The lookup may load the library's code on that device, which a stream
+// capture must not record: a first call made while `stream` is capturing is
+// refused (MVLLM_ERR_INVALID) before any runtime call but the capture query.
 int scratch_address(hipStream_t stream, void** out) {
   static std::mutex mu;
   static void* per_device[64] = {nullptr};
@@ -475,6 +478,12 @@ int scratch_address(hipStream_t stream, void** out) {
   if (dev < 0 || dev >= 64) return fail(MVLLM_ERR_INVALID, "device %d out of range", dev);
   std::lock_guard<std::mutex> lock(mu);
   if (!per_device[dev]) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    MVLLM_HIP_TRY(hipStreamIsCapturing(stream, &capture));
+    if (capture != hipStreamCaptureStatusNone)
+      return fail(MVLLM_ERR_INVALID,
+                  "mvllm_attention_forward_noalloc: the first call on device %d is under stream capture; "
+                  "call it once outside capture on that device (it looks up its workspace then)", dev);
     int current = 0;
     MVLLM_HIP_TRY(hipGetDevice(&current));
     if (current != dev) MVLLM_HIP_TRY(hipSetDevice(dev));
