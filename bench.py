@@ -1013,6 +1013,16 @@ def main() -> int:
         result["overlap"] = overlap
     if args.workload in PREFILL_WORKLOADS:
         result["prefill"] = prefill_record(w, serial)
+        if not bool((w.query_lengths == 1).any()) and result["prefill"].get("kernel_us"):
+            # No decode request: the decode launch finds no work, so the
+            # step is priced by its FLOPs and the prefill kernel is the
+            # roofline.
+            flops = result["prefill"]["flops"]
+            result["unit"] = "TFLOP/s"
+            result["value"] = round(flops / (ms_per_step * 1e-3) / 1e12, 2)
+            result["roofline"] = {k: result["prefill"][k] for k in
+                                  ("kernel", "bound", "achieved", "peak", "unit", "frac", "kernel_us", "flops")}
+            result["roofline"]["traffic"] = None
         if not args.no_cpu_baseline:
             result["prefill"]["cpu_baseline"] = cpu_prefill_baseline(w)
         from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention

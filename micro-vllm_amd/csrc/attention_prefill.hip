@@ -102,16 +102,27 @@ template <> struct Mma32<f16_t> {
   }
 };
 
+// Minimum / maximum over the wave, in every lane, with no LDS round trip:
+// DPP quad permutes [1,0,3,2] and [2,3,0,1], then the 8- and 16-lane mirrors,
+// then the 16- and 32-lane swaps.
+template <typename Op>
+__device__ __forceinline__ int32_t wave_reduce_i(int32_t v, Op op) {
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));
+  v = op(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+  v = op(static_cast<int32_t>(r16[0]), static_cast<int32_t>(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+  return op(static_cast<int32_t>(r32[0]), static_cast<int32_t>(r32[1]));
+}
+
 __device__ __forceinline__ int32_t wave_min_i(int32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m, 64));
-  return v;
+  return wave_reduce_i(v, [](int32_t x, int32_t y) { return x < y ? x : y; });
 }
 
 __device__ __forceinline__ int32_t wave_max_i(int32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
-  return v;
+  return wave_reduce_i(v, [](int32_t x, int32_t y) { return x > y ? x : y; });
 }
 
 // LDS byte offset of 16-byte chunk `chunk` of tile row `row` (256-byte rows).

@@ -238,8 +238,7 @@ __device__ __forceinline__ void decode_split_lds_body(const AttnArgs& a, uint8_t
     for (int e = 0; e < 4; ++e)
       s[e] = ((okmask >> (4 * grp + e)) & 1u) ? sc[e] * a.scale_log2 : -INFINITY;
     float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    bm = fmaxf(bm, shfl_xor_f(bm, 16));
-    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    bm = max_xor32_f(max_xor16_f(bm));
     const float mn = fmaxf(m, bm);
     const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
     float p[4];
@@ -287,8 +286,7 @@ __device__ __forceinline__ void decode_split_lds_body(const AttnArgs& a, uint8_t
     compiler_fence();
   }
 
-  const float l2 = l + shfl_xor_f(l, 16);
-  const float lt = l2 + shfl_xor_f(l2, 32);
+  const float lt = sum_xor32_f(sum_xor16_f(l));
   if (col >= G) return;
   write_decode_result<T>(a, r, qs, hq, split, item.ns, m, lt, acc, grp);
 }

@@ -203,6 +203,12 @@ class GenerationEngine:
         # Synchronous decode-only steps skip the plan objects (see
         # _fast_decode_step); False forces every step through schedule().
         self.fast_decode = True
+        # Arrays of the running requests carried from one fast step to the
+        # next (valid while no other step changes the running set).
+        self._fast_state: _FastState | None = None
+        # Reused host (pinned) and device payload buffers of fast steps.
+        self._fast_payload: tuple[torch.Tensor, torch.Tensor] | None = None
+        self._fast_event: torch.cuda.Event | None = None
         self.fast_decode_steps = 0
         self.fast_phase_seconds = {"schedule": 0.0, "pack": 0.0, "replay": 0.0, "overlap": 0.0, "wait": 0.0,
                                    "append": 0.0}
@@ -301,6 +307,7 @@ class GenerationEngine:
         )
 
     def schedule(self) -> SchedulerOutput:
+        self._fast_state = None
         budget = self.max_num_batched_tokens
         scheduled: list[ScheduledRequest] = []
         preempted: list[str] = []
@@ -500,8 +507,10 @@ class GenerationEngine:
         (no preemption). The step then does what schedule() + execute() +
         _update() do, in the same order (blocks allocated in running order;
         per request: count, prefix-cache commit, finish and free), with the
-        packing arrays built by numpy from the requests instead of one plan
-        object per request. The bookkeeping that does not need the sampled
+        packing arrays held by numpy instead of one plan object per request:
+        built from the requests, or carried from the previous fast step (each
+        request one token further, finished ones dropped; any planned step
+        discards them). The bookkeeping that does not need the sampled
         tokens runs while the GPU computes them; the tokens are appended
         after the step's device-to-host copy completes, so the step still
         ends synchronized with its tokens on the host."""
@@ -521,42 +530,62 @@ class GenerationEngine:
         ):
             return False
         t0 = time.perf_counter()
-        computed = np.fromiter((r.num_computed_tokens for r in running), np.int64, n)
-        known = np.fromiter((len(r.token_ids) for r in running), np.int64, n)
-        if not np.array_equal(known - computed, np.ones(n, np.int64)):
-            return False
         bs = self.block_size
-        nblk = np.fromiter((len(r.block_ids) for r in running), np.int64, n)
+        state = self._fast_state
+        if state is not None and state.running is running:
+            # The previous fast step left every request one known token past
+            # its computed ones; its arrays are this step's.
+            computed, nblk, slots, tokens = state.computed, state.nblk, state.slots, state.tokens
+            stale = set(state.dirty)
+        else:
+            computed = np.fromiter((r.num_computed_tokens for r in running), np.int64, n)
+            known = np.fromiter((len(r.token_ids) for r in running), np.int64, n)
+            if not np.array_equal(known - computed, np.ones(n, np.int64)):
+                return False
+            nblk = np.fromiter((len(r.block_ids) for r in running), np.int64, n)
+            if self.block_rows is None:
+                self.block_rows = DeviceBlockRows(self.max_num_seqs, -(-self.max_model_len // bs), self.model.device)
+            slots = np.fromiter((self.block_rows.slot(r.request_id) for r in running), np.int64, n)
+            tokens = np.fromiter((r.token_ids[-1] for r in running), np.int64, n)
+            first = np.fromiter(
+                (r.row_sent if r.row_dirty is None else min(r.row_sent, r.row_dirty) for r in running), np.int64, n
+            )
+            stale = set(np.nonzero(first < nblk)[0].tolist())
+        self._fast_state = None
         short = np.nonzero(computed + 1 > nblk * bs)[0]
         if len(short):
             need = int(((computed[short] + bs) // bs - nblk[short]).sum())
             if need > self.pool.num_free_blocks:
                 return False  # schedule() preempts
+            nblk = nblk.copy()
             for i in short.tolist():
                 if not self._ensure_blocks(running[i], int(computed[i]) + 1):
                     raise RuntimeError("block pool changed during a decode step")
                 nblk[i] = len(running[i].block_ids)
-        if self.block_rows is None:
-            self.block_rows = DeviceBlockRows(self.max_num_seqs, -(-self.max_model_len // bs), self.model.device)
+                stale.add(i)
         rows = self.block_rows
-        slots = np.fromiter((rows.slot(r.request_id) for r in running), np.int64, n)
-        first = np.fromiter(
-            (r.row_sent if r.row_dirty is None else min(r.row_sent, r.row_dirty) for r in running), np.int64, n
-        )
         updates = []
-        for i in np.nonzero(first < nblk)[0].tolist():
-            r, f, k = running[i], int(first[i]), int(nblk[i])
-            updates.append((int(slots[i]), f, r.block_ids[f:k]))
+        for i in sorted(stale):
+            r = running[i]
+            f = r.row_sent if r.row_dirty is None else min(r.row_sent, r.row_dirty)
+            k = len(r.block_ids)
+            if f < k:
+                updates.append((int(slots[i]), f, r.block_ids[f:k]))
             r.row_sent, r.row_dirty = k, None
-        tokens = np.fromiter((r.token_ids[-1] for r in running), np.int64, n)
 
         size = g.bucket(n)
         entry = g.entries.get(size) or g.capture(size)
         t_pack = time.perf_counter()
+        if self._fast_payload is None:
+            words = 4096 + self.max_num_seqs * (2 + 8) + 4 * self.max_num_seqs
+            self._fast_payload = (
+                torch.empty(words, dtype=torch.int32, pin_memory=True),
+                torch.empty(words, dtype=torch.int32, device=self.model.device),
+            )
         with torch.inference_mode():
             pack_decode_rows(
                 tokens, computed, nblk, slots, updates, spec=FullAttentionSpec(), block_size=bs,
-                null_block_id=self.null_block_id, block_rows=rows, into=entry.buffers,
+                null_block_id=self.null_block_id, block_rows=rows, into=entry.buffers, staging=self._fast_payload,
             )
             t_replay = time.perf_counter()
             self.pack_seconds += t_replay - t_pack
@@ -564,28 +593,47 @@ class GenerationEngine:
             host = g._host[g._flip]
             g._flip ^= 1
             host[:n].copy_(entry.tokens[:n], non_blocking=True)
-            done = torch.cuda.Event()
+            if self._fast_event is None:
+                self._fast_event = torch.cuda.Event()
+            done = self._fast_event
             done.record()
         t1 = time.perf_counter()
 
         # While the GPU runs: _update's per-request work that needs no token.
         finished = []
-        for r in running:
+        dirty = []
+        for i, r in enumerate(running):
             r.num_computed_tokens += 1
             if self.enable_prefix_cache:
                 self._commit(r)
+                if r.row_dirty is not None:
+                    dirty.append(i)
             if len(r.output_token_ids) + 1 >= r.max_tokens:
-                finished.append(r)
+                finished.append(i)
                 self._free(r)
+        # The next fast step's arrays, every request one token further (its
+        # last tokens are filled in once this step's arrive).
         if finished:
-            gone = set(map(id, finished))
-            self._running = [r for r in running if id(r) not in gone]
+            gone = set(finished)
+            self._running = [r for i, r in enumerate(running) if i not in gone]
+            keep = np.setdiff1d(np.arange(n), np.asarray(finished))
+            remap = {int(old_i): new_i for new_i, old_i in enumerate(keep)}
+            state = _FastState(
+                self._running, computed[keep] + 1, nblk[keep], slots[keep], None,
+                [remap[i] for i in dirty if i in remap],
+            )
+        else:
+            keep = None
+            state = _FastState(self._running, computed + 1, nblk, slots, None, dirty)
         t2 = time.perf_counter()
         done.synchronize()
         t3 = time.perf_counter()
-        for r, token in zip(running, host[:n].tolist()):
+        sampled = host[:n].numpy().copy()
+        for r, token in zip(running, sampled.tolist()):
             r.output_token_ids.append(token)
             r.token_ids.append(token)
+        state.tokens = sampled if keep is None else sampled[keep]
+        self._fast_state = state
         t4 = time.perf_counter()
         ph = self.fast_phase_seconds
         ph["schedule"] += t_pack - t0
@@ -762,6 +810,20 @@ class DecodeGraphs:
         event = torch.cuda.Event()
         event.record()
         return PendingStep(host, event)
+
+
+@dataclass
+class _FastState:
+    """Arrays of the running requests, in order, carried between fast decode
+    steps: computed tokens, block counts, block-row slots, last tokens, and
+    the indices whose block rows the prefix cache changed."""
+
+    running: list
+    computed: np.ndarray
+    nblk: np.ndarray
+    slots: np.ndarray
+    tokens: np.ndarray
+    dirty: list
 
 
 @dataclass

@@ -351,6 +351,7 @@ def pack_decode_rows(
     null_block_id: int,
     block_rows: DeviceBlockRows,
     into: PackedBatch,
+    staging: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> PackedBatch:
     """Pack a decode-only step (every request: one token, sampled) from
     per-request arrays, without a ``SchedulerOutput``: the same launch and
@@ -359,7 +360,10 @@ def pack_decode_rows(
     ``token_ids[r]``, ``computed[r]`` computed tokens and
     ``block_lengths[r]`` block ids in block row ``slots[r]``.
     ``row_updates`` lists ``(slot, first, ids)``: the ids that changed in a
-    row since it was last written."""
+    row since it was last written. ``staging`` (pinned host int32, device
+    int32) carries the payload without allocating when it fits; the caller
+    guarantees that the previous copy out of it and the previous pack
+    launch reading it have completed."""
 
     device = into.input_ids.device
     n = int(len(token_ids))
@@ -386,14 +390,25 @@ def pack_decode_rows(
         records[i] = (slot, first, k, ids_offset)
         ids_offset += k
     ids = np.fromiter(chain.from_iterable(u[2] for u in row_updates), dtype=np.int32, count=total_blocks)
-    host = torch.from_numpy(np.concatenate((np.asarray(token_ids, np.int32), info.reshape(-1), ids, records.reshape(-1))))
-    if host.numel() == 0:
-        host = torch.zeros(1, dtype=torch.int32)
-    payload = host.pin_memory().to(device, non_blocking=True)
-    base = payload.data_ptr()
     info_offset = n
     ids_at = n + info.size
     updates_offset = ids_at + total_blocks
+    words = updates_offset + records.size
+    if staging is not None and 0 < words <= staging[0].numel() <= staging[1].numel():
+        hbuf, dbuf = staging
+        hv = hbuf.numpy()
+        hv[:n] = token_ids
+        hv[info_offset:ids_at] = info.reshape(-1)
+        hv[ids_at:updates_offset] = ids
+        hv[updates_offset:words] = records.reshape(-1)
+        dbuf[:words].copy_(hbuf[:words], non_blocking=True)
+        payload = dbuf
+    else:
+        host = torch.from_numpy(np.concatenate((np.asarray(token_ids, np.int32), info.reshape(-1), ids, records.reshape(-1))))
+        if host.numel() == 0:
+            host = torch.zeros(1, dtype=torch.int32)
+        payload = host.pin_memory().to(device, non_blocking=True)
+    base = payload.data_ptr()
     args = _pack_args(
         into, 0, spec, base, info_offset=info_offset, ids_offset=ids_at, total_blocks=total_blocks, num_requests=n,
         num_tokens=n, num_sampling=n, block_size=block_size, null_block_id=null_block_id,
