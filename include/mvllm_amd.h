@@ -384,19 +384,23 @@ int mvllm_add_rms_norm(const void* x, int64_t x_stride, void* residual,
 /*
  * Pre-attention step of one layer, head_dim 128: per token, per-head RMSNorm
  * of query and key (weights may both be NULL: no norm), rotary embedding with
- * float32 cos/sin tables [num_tokens, 128] (both NULL: none; rotate-half
+ * float32 cos/sin tables of 128 values per row (both NULL: none; rotate-half
  * convention), the rotated query to q_out ([num_tokens, Hq, 128],
  * contiguous), and the rotated key and the value into their paged-cache slot
- * (slot < 0 or out of range writes nothing). Replaces Qwen3Attention's q/k
- * norm + RotaryEmbedding (models/qwen.py:89-91, layers/rotary_embedding.py:
- * 14-52) followed by write_kv_cache (operators/reference.py:84-98); the
- * attention that follows is mvllm_paged_attention.
+ * (slot < 0 or out of range writes nothing). With positions == NULL the
+ * tables hold one row per token; otherwise they hold table_rows rows, token t
+ * uses row positions[t], and a position outside [0, table_rows) rotates to
+ * NaN (never an out-of-bounds read). Replaces Qwen3Attention's q/k norm +
+ * RotaryEmbedding (models/qwen.py:89-91, layers/rotary_embedding.py:14-52)
+ * followed by write_kv_cache (operators/reference.py:84-98); the attention
+ * that follows is mvllm_paged_attention.
  */
 int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query,
                                 const mvllm_tensor3* key,
                                 const mvllm_tensor3* value,
                                 const void* q_weight, const void* k_weight,
                                 const float* cos_table, const float* sin_table,
+                                const int64_t* positions, int64_t table_rows,
                                 float eps, void* q_out,
                                 const mvllm_kv_cache* cache,
                                 const int64_t* slot_mapping, void* stream);
@@ -410,13 +414,43 @@ int mvllm_silu_mul(const void* gate_up, int64_t in_stride, void* out,
                    int64_t out_stride, int64_t rows, int64_t intermediate,
                    int32_t dtype, void* stream);
 
+/*
+ * Embedding lookup + the first decoder layer's input RMSNorm, bf16/fp16:
+ * residual_out[t] = embedding[id_t] and out[t] = RMSNorm(residual_out[t])
+ * with the rounding of mvllm_add_rms_norm (residual == NULL), where id_t =
+ * ids[t], or last_tokens[r] when ids[t] = -(1 + r) (a placeholder for the
+ * token sampled at row r of the previous step, r < last_count). An id
+ * outside [0, vocab) gives a zero row. Needs dim and the row strides in
+ * multiples of 8 elements and 16-byte aligned rows. Replaces embed_tokens
+ * and the first input_layernorm (models/qwen.py:227 and :144,
+ * layers/normalization.py:7-22).
+ */
+int mvllm_embed_rms_norm(const int64_t* ids, int64_t num_tokens,
+                         const int64_t* last_tokens, int64_t last_count,
+                         const void* embedding, int64_t vocab,
+                         int64_t embedding_stride, const void* weight,
+                         void* residual_out, int64_t residual_stride,
+                         void* out, int64_t out_stride, int64_t dim,
+                         float eps, int32_t dtype, void* stream);
+
+/*
+ * Greedy sampling: out[r] = torch.argmax(logits[r, :cols]) for each of
+ * `rows` rows (row_stride in elements; bf16, fp16 or fp32), the first index
+ * of the maximum, a NaN counting as the maximum. out_copy (may be NULL)
+ * receives the same indices. Replaces the sampler's per-row argmax
+ * (sampling/sampler.py:24-31, 39-46); one launch, no host sync.
+ */
+int mvllm_argmax_rows(const void* logits, int64_t rows, int64_t cols,
+                      int64_t row_stride, int32_t dtype, int64_t* out,
+                      int64_t* out_copy, void* stream);
+
 /* Text of the last failure on this thread ("" if none). */
 const char* mvllm_last_error(void);
 
 /* ABI version of this header (bumped on incompatible change). */
 int mvllm_abi_version(void);
 
-#define MVLLM_ABI_VERSION 4
+#define MVLLM_ABI_VERSION 5
 
 #ifdef __cplusplus
 }

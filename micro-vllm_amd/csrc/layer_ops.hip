@@ -12,6 +12,11 @@
 //   14-52), q to its output, rotated k and v straight into their paged-cache
 //   slot (reference.py:84-98; slot < 0 writes nothing).
 // * silu_mul: out = round(round(silu(gate)) * up) (layers/mlp.py:10-21).
+// * embed_rms_norm: the embedding rows of a step's token ids (models/qwen.py:
+//   227 embed_tokens) and the first layer's input RMSNorm (:144), one pass.
+// * argmax_rows: greedy sampling, torch.argmax(logits, dim=-1) per row
+//   (sampling/sampler.py:24-31, 39-46): the first index of the row's maximum, NaN
+//   counted as the maximum.
 #include <cmath>
 
 #include "common.h"
@@ -48,6 +53,15 @@ struct NormArgs {
   int64_t rows;
   int32_t dim;
   float eps;
+  // Gather mode only: row t of x is row ids[t] of the embedding table x; an
+  // id -(1 + r) is a placeholder for last[r]. Ids outside [0, vocab) after
+  // that give a zero row. The gathered rows also go to copy_out.
+  const int64_t* ids;
+  const int64_t* last;
+  int64_t last_count;
+  int64_t vocab;
+  uint16_t* copy_out;
+  int64_t copy_stride;
 };
 
 constexpr int kNormThreads = 256;
@@ -97,12 +111,24 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(NormArgs a) 
 // Vectorised form: one wave per row, lane l holds dims 8 (l + 64 c) .. +8
 // for chunk c < CHUNKS (dim <= 512 CHUNKS), 16-byte loads and stores. Needs
 // dim % 8 == 0 and 16-byte aligned rows; the kernel above covers the rest.
-template <typename T, int CHUNKS>
+// GATHER: x rows come from the embedding table by token id (no residual);
+// the normalisation is the same code, so it rounds as add_rms_norm does.
+template <typename T, int CHUNKS, bool GATHER>
 __global__ __launch_bounds__(256) void add_rms_norm_rows_kernel(NormArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const uint16_t* x = a.x + row * a.x_stride;
+  bool x_ok = true;
+  if constexpr (GATHER) {
+    int64_t id = a.ids[row];
+    if (id < 0) {
+      const int64_t r = -(id + 1);
+      id = (a.last != nullptr && r < a.last_count) ? a.last[r] : -1;
+    }
+    x_ok = id >= 0 && id < a.vocab;
+    x = a.x + (x_ok ? id : 0) * a.x_stride;
+  }
   uint16_t* res = a.residual ? a.residual + row * a.res_stride : nullptr;
   float h[CHUNKS][8];
   float sq = 0.f;
@@ -112,7 +138,9 @@ __global__ __launch_bounds__(256) void add_rms_norm_rows_kernel(NormArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) h[c][e] = 0.f;
     if (d < a.dim) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(x + d);
+      uint4 xv = uint4{0u, 0u, 0u, 0u};
+      if (x_ok) xv = *reinterpret_cast<const uint4*>(x + d);
+      if constexpr (GATHER) *reinterpret_cast<uint4*>(a.copy_out + row * a.copy_stride + d) = xv;
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[c][e] = Act<T>::load((xw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
@@ -163,8 +191,10 @@ struct QkArgs {
   int64_t q_s0, q_s1, k_s0, k_s1, v_s0, v_s1;
   const uint16_t* q_weight;  // [D] or null (no q/k norm)
   const uint16_t* k_weight;
-  const float* cos;  // [N, D] or null (no rotary embedding)
+  const float* cos;  // [table_rows, D] or null (no rotary embedding)
   const float* sin;
+  const int64_t* pos;  // table row of token t: pos[t] (null: row t)
+  int64_t table_rows;
   uint16_t* q_out;  // [N, Hq, D] contiguous
   uint16_t* cache;
   int64_t c_s[5];
@@ -207,8 +237,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(QkArgs a) {
       const float p0 = __shfl_xor(x0, 32, 64), p1 = __shfl_xor(x1, 32, 64);
       // rotate_half: dims < 64 take -x[d + 64], dims >= 64 take x[d - 64].
       const float r0 = lane < 32 ? -p0 : p0, r1 = lane < 32 ? -p1 : p1;
-      const float2 c = *reinterpret_cast<const float2*>(a.cos + t * 128 + 2 * lane);
-      const float2 s = *reinterpret_cast<const float2*>(a.sin + t * 128 + 2 * lane);
+      const int64_t tr = a.pos ? a.pos[t] : t;
+      float2 c = make_float2(NAN, NAN), s = c;  // a position outside the table gives NaN
+      if (tr >= 0 && tr < a.table_rows) {
+        c = *reinterpret_cast<const float2*>(a.cos + tr * 128 + 2 * lane);
+        s = *reinterpret_cast<const float2*>(a.sin + tr * 128 + 2 * lane);
+      }
       x0 = __fadd_rn(__fmul_rn(x0, c.x), __fmul_rn(r0, s.x));
       x1 = __fadd_rn(__fmul_rn(x1, c.y), __fmul_rn(r1, s.y));
     }
@@ -246,9 +280,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_token_kernel(QkArgs a) {
   const int g = lane >> 4, j = lane & 15;
   float cv[8], sv[8];
   if (a.cos) {
-    const float4* cp = reinterpret_cast<const float4*>(a.cos + t * 128 + 8 * j);
-    const float4* sp = reinterpret_cast<const float4*>(a.sin + t * 128 + 8 * j);
-    const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+    const int64_t tr = a.pos ? a.pos[t] : t;
+    float4 c0 = make_float4(NAN, NAN, NAN, NAN), c1 = c0, s0 = c0, s1 = c0;  // outside the table: NaN
+    if (tr >= 0 && tr < a.table_rows) {
+      const float4* cp = reinterpret_cast<const float4*>(a.cos + tr * 128 + 8 * j);
+      const float4* sp = reinterpret_cast<const float4*>(a.sin + tr * 128 + 8 * j);
+      c0 = cp[0]; c1 = cp[1]; s0 = sp[0]; s1 = sp[1];
+    }
     cv[0] = c0.x; cv[1] = c0.y; cv[2] = c0.z; cv[3] = c0.w; cv[4] = c1.x; cv[5] = c1.y; cv[6] = c1.z; cv[7] = c1.w;
     sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
   }
@@ -343,21 +381,140 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(SiluArgs a) {
       static_cast<uint32_t>(Act<T>::store(r[0])) | (static_cast<uint32_t>(Act<T>::store(r[1])) << 16);
 }
 
+// ------------------------------------------------------------ argmax_rows
+
+struct ArgmaxArgs {
+  const uint8_t* logits;
+  int64_t rows, cols, row_stride;  // strides in elements
+  int64_t* out;
+  int64_t* out_copy;  // null: none
+  int32_t esize;
+  bool vec;  // 16-byte aligned rows: 16-byte loads
+};
+
+constexpr int kArgmaxThreads = 1024;
+constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
+
+template <typename T> struct Logit;
+template <> struct Logit<bf16_t> {
+  static constexpr int kPerVec = 8;
+  __device__ static float get(const uint4& v, int e) {
+    const uint32_t w = (&v.x)[e >> 1];
+    return bf16_bits_to_float((w >> (16 * (e & 1))) & 0xFFFFu);
+  }
+  __device__ static float get1(const uint8_t* p) { return bf16_bits_to_float(*reinterpret_cast<const uint16_t*>(p)); }
+};
+template <> struct Logit<f16_t> {
+  static constexpr int kPerVec = 8;
+  __device__ static float get(const uint4& v, int e) {
+    const uint32_t w = (&v.x)[e >> 1];
+    return f16_bits_to_float((w >> (16 * (e & 1))) & 0xFFFFu);
+  }
+  __device__ static float get1(const uint8_t* p) { return f16_bits_to_float(*reinterpret_cast<const uint16_t*>(p)); }
+};
+template <> struct Logit<float> {
+  static constexpr int kPerVec = 4;
+  __device__ static float get(const uint4& v, int e) { return __uint_as_float((&v.x)[e]); }
+  __device__ static float get1(const uint8_t* p) { return *reinterpret_cast<const float*>(p); }
+};
+
+// Running (maximum, first index) of one lane over indices in increasing
+// order: a value replaces the maximum only if strictly greater, so the first
+// of equal values stays (-0 and +0 compare equal, as in torch); the first
+// NaN is kept aside, since NaN is the maximum.
+struct ArgmaxLane {
+  float best = -INFINITY;
+  uint32_t best_idx = kNoIndex;
+  uint32_t nan_idx = kNoIndex;
+  __device__ void see(float v, uint32_t idx) {
+    if (best_idx == kNoIndex || v > best) {
+      best = v != v ? best : v;
+      best_idx = v != v ? best_idx : idx;
+    }
+    if (v != v && nan_idx == kNoIndex) nan_idx = idx;
+  }
+  // One 64-bit key that orders candidates across lanes: the value, mapped to
+  // an unsigned integer that sorts like the float (NaN above +inf, -0 = +0),
+  // then the complement of the index, so that equal values prefer the
+  // smaller index. 0 = no candidate.
+  __device__ uint64_t key() const {
+    if (nan_idx != kNoIndex) return (0xFFFFFFFFull << 32) | (0xFFFFFFFFu - nan_idx);
+    if (best_idx == kNoIndex) return 0;
+    uint32_t b = __float_as_uint(best);
+    if ((b & 0x7FFFFFFFu) == 0) b = 0;
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<uint64_t>(ord) << 32) | (0xFFFFFFFFu - best_idx);
+  }
+};
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// One workgroup per row: 16-byte loads, four in flight per lane, then a
+// 64-bit maximum over the workgroup.
+template <typename T>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(ArgmaxArgs a) {
+  const int64_t row = blockIdx.x;
+  const uint8_t* base = a.logits + row * a.row_stride * a.esize;
+  ArgmaxLane lane_state;
+  const int tid = threadIdx.x;
+  if (a.vec) {
+    constexpr int P = Logit<T>::kPerVec;
+    const int64_t nvec = a.cols / P;
+    const uint4* vp = reinterpret_cast<const uint4*>(base);
+    for (int64_t v0 = tid; v0 < nvec; v0 += 4LL * kArgmaxThreads) {
+      uint4 buf[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t v = v0 + static_cast<int64_t>(u) * kArgmaxThreads;
+        buf[u] = v < nvec ? vp[v] : uint4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t v = v0 + static_cast<int64_t>(u) * kArgmaxThreads;
+        if (v < nvec) {
+#pragma unroll
+          for (int e = 0; e < P; ++e) lane_state.see(Logit<T>::get(buf[u], e), static_cast<uint32_t>(v * P + e));
+        }
+      }
+    }
+    // The tail past the last whole vector, by the first lanes.
+    const int64_t tail = nvec * P + tid;
+    if (tail < a.cols) lane_state.see(Logit<T>::get1(base + tail * a.esize), static_cast<uint32_t>(tail));
+  } else {
+    for (int64_t c = tid; c < a.cols; c += kArgmaxThreads)
+      lane_state.see(Logit<T>::get1(base + c * a.esize), static_cast<uint32_t>(c));
+  }
+  uint64_t k = lane_state.key();
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) k = max_u64(k, __shfl_xor(k, m, 64));
+  __shared__ uint64_t wave_best[kArgmaxThreads / 64];
+  if ((tid & 63) == 0) wave_best[tid >> 6] = k;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int w = 0; w < kArgmaxThreads / 64; ++w) best = max_u64(best, wave_best[w]);
+    const int64_t idx = static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(best & 0xFFFFFFFFu));
+    a.out[row] = idx;
+    if (a.out_copy) a.out_copy[row] = idx;
+  }
+}
+
 bool half_dtype(int32_t d) { return d == MVLLM_DTYPE_BF16 || d == MVLLM_DTYPE_F16; }
 
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 bool mult8(int64_t v) { return (v & 7) == 0; }
 
-template <typename T>
+template <typename T, bool GATHER = false>
 int launch_add_rms_norm_rows(const NormArgs& a, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
   const int chunks = (a.dim + 511) / 512;
-  if (chunks <= 1) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 1>), grid, dim3(256), 0, s, a);
-  else if (chunks <= 2) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 2>), grid, dim3(256), 0, s, a);
-  else if (chunks <= 4) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 4>), grid, dim3(256), 0, s, a);
-  else if (chunks <= 8) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 8>), grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 16>), grid, dim3(256), 0, s, a);
+  if (chunks <= 1) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 1, GATHER>), grid, dim3(256), 0, s, a);
+  else if (chunks <= 2) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 2, GATHER>), grid, dim3(256), 0, s, a);
+  else if (chunks <= 4) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 4, GATHER>), grid, dim3(256), 0, s, a);
+  else if (chunks <= 8) hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 8, GATHER>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((add_rms_norm_rows_kernel<T, 16, GATHER>), grid, dim3(256), 0, s, a);
   MVLLM_LAUNCH_CHECK("add_rms_norm_rows_kernel");
   return MVLLM_OK;
 }
@@ -378,9 +535,17 @@ extern "C" int mvllm_add_rms_norm(const void* x, int64_t x_stride, void* residua
   if (rows == 0) return MVLLM_OK;
   if (!x || !weight || !out) return fail(MVLLM_ERR_INVALID, "add_rms_norm: null pointer");
   if (rows > INT32_MAX) return fail(MVLLM_ERR_INVALID, "add_rms_norm: too many rows");
-  NormArgs a{static_cast<const uint16_t*>(x), static_cast<uint16_t*>(residual),
-             static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), x_stride, residual_stride,
-             out_stride, rows, static_cast<int32_t>(dim), eps};
+  NormArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.residual = static_cast<uint16_t*>(residual);
+  a.weight = static_cast<const uint16_t*>(weight);
+  a.out = static_cast<uint16_t*>(out);
+  a.x_stride = x_stride;
+  a.res_stride = residual_stride;
+  a.out_stride = out_stride;
+  a.rows = rows;
+  a.dim = static_cast<int32_t>(dim);
+  a.eps = eps;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool vec = mult8(dim) && mult8(x_stride) && mult8(out_stride) && aligned16(x) && aligned16(weight) &&
                    aligned16(out) && (!residual || (mult8(residual_stride) && aligned16(residual)));
@@ -397,7 +562,8 @@ extern "C" int mvllm_add_rms_norm(const void* x, int64_t x_stride, void* residua
 extern "C" int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query, const mvllm_tensor3* key,
                                            const mvllm_tensor3* value, const void* q_weight,
                                            const void* k_weight, const float* cos_table,
-                                           const float* sin_table, float eps, void* q_out,
+                                           const float* sin_table, const int64_t* positions,
+                                           int64_t table_rows, float eps, void* q_out,
                                            const mvllm_kv_cache* cache, const int64_t* slot_mapping,
                                            void* stream) {
   clear_error();
@@ -417,6 +583,8 @@ extern "C" int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query, const mvl
     return fail(MVLLM_ERR_INVALID, "qk_norm_rope: rows must be contiguous with even strides");
   if ((cos_table == nullptr) != (sin_table == nullptr) || (q_weight == nullptr) != (k_weight == nullptr))
     return fail(MVLLM_ERR_INVALID, "qk_norm_rope: cos/sin and q/k weights come in pairs");
+  if (positions && (!cos_table || table_rows <= 0))
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: positions need cos/sin tables of table_rows > 0 rows");
   if (N == 0) return MVLLM_OK;
   if (!slot_mapping || !q_out || !cache->data || !aligned4(query->data) || !aligned4(key->data) ||
       !aligned4(value->data) || !aligned4(q_out) || !aligned4(cache->data))
@@ -432,6 +600,8 @@ extern "C" int mvllm_qk_norm_rope_kv_write(const mvllm_tensor3* query, const mvl
   a.k_weight = static_cast<const uint16_t*>(k_weight);
   a.cos = cos_table;
   a.sin = sin_table;
+  a.pos = positions;
+  a.table_rows = positions ? table_rows : N;
   a.q_out = static_cast<uint16_t*>(q_out);
   a.cache = static_cast<uint16_t*>(cache->data);
   for (int i = 0; i < 5; ++i) a.c_s[i] = cache->stride[i];
@@ -495,5 +665,76 @@ extern "C" int mvllm_silu_mul(const void* gate_up, int64_t in_stride, void* out,
   else
     hipLaunchKernelGGL(silu_mul_kernel<f16_t>, grid, dim3(256), 0, s, a);
   MVLLM_LAUNCH_CHECK("silu_mul_kernel");
+  return MVLLM_OK;
+}
+
+extern "C" int mvllm_embed_rms_norm(const int64_t* ids, int64_t num_tokens, const int64_t* last_tokens,
+                                    int64_t last_count, const void* embedding, int64_t vocab,
+                                    int64_t embedding_stride, const void* weight, void* residual_out,
+                                    int64_t residual_stride, void* out, int64_t out_stride, int64_t dim,
+                                    float eps, int32_t dtype, void* stream) {
+  clear_error();
+  if (!half_dtype(dtype)) return fail(MVLLM_ERR_UNSUPPORTED, "embed_rms_norm needs bf16 or fp16");
+  if (num_tokens < 0 || vocab <= 0 || last_count < 0 || dim <= 0 || dim > 8192)
+    return fail(MVLLM_ERR_INVALID, "embed_rms_norm: sizes out of range");
+  if (num_tokens == 0) return MVLLM_OK;
+  if (!ids || !embedding || !weight || !residual_out || !out || (last_count > 0 && !last_tokens))
+    return fail(MVLLM_ERR_INVALID, "embed_rms_norm: null pointer");
+  if (num_tokens > INT32_MAX) return fail(MVLLM_ERR_INVALID, "embed_rms_norm: too many tokens");
+  if (!mult8(dim) || !mult8(embedding_stride) || !mult8(residual_stride) || !mult8(out_stride) ||
+      !aligned16(embedding) || !aligned16(weight) || !aligned16(residual_out) || !aligned16(out))
+    return fail(MVLLM_ERR_UNSUPPORTED, "embed_rms_norm needs dim and row strides in multiples of 8 elements "
+                                       "and 16-byte aligned rows");
+  NormArgs a{};
+  a.x = static_cast<const uint16_t*>(embedding);
+  a.weight = static_cast<const uint16_t*>(weight);
+  a.out = static_cast<uint16_t*>(out);
+  a.x_stride = embedding_stride;
+  a.out_stride = out_stride;
+  a.rows = num_tokens;
+  a.dim = static_cast<int32_t>(dim);
+  a.eps = eps;
+  a.ids = ids;
+  a.last = last_count > 0 ? last_tokens : nullptr;
+  a.last_count = last_count;
+  a.vocab = vocab;
+  a.copy_out = static_cast<uint16_t*>(residual_out);
+  a.copy_stride = residual_stride;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == MVLLM_DTYPE_BF16) return launch_add_rms_norm_rows<bf16_t, true>(a, s);
+  return launch_add_rms_norm_rows<f16_t, true>(a, s);
+}
+
+extern "C" int mvllm_argmax_rows(const void* logits, int64_t rows, int64_t cols, int64_t row_stride,
+                                 int32_t dtype, int64_t* out, int64_t* out_copy, void* stream) {
+  clear_error();
+  const int32_t esize = dtype == MVLLM_DTYPE_F32 ? 4 : half_dtype(dtype) ? 2 : 0;
+  if (!esize) return fail(MVLLM_ERR_UNSUPPORTED, "argmax_rows needs bf16, fp16 or fp32 logits");
+  if (rows < 0 || cols <= 0 || cols > INT32_MAX || row_stride < cols)
+    return fail(MVLLM_ERR_INVALID, "argmax_rows: rows %lld / cols %lld / row stride %lld out of range",
+                (long long)rows, (long long)cols, (long long)row_stride);
+  if (rows == 0) return MVLLM_OK;
+  if (!logits || !out) return fail(MVLLM_ERR_INVALID, "argmax_rows: null pointer");
+  if (rows > INT32_MAX) return fail(MVLLM_ERR_INVALID, "argmax_rows: too many rows");
+  if ((reinterpret_cast<uintptr_t>(logits) & (esize - 1)) != 0)
+    return fail(MVLLM_ERR_INVALID, "argmax_rows: misaligned logits");
+  ArgmaxArgs a{};
+  a.logits = static_cast<const uint8_t*>(logits);
+  a.rows = rows;
+  a.cols = cols;
+  a.row_stride = row_stride;
+  a.out = out;
+  a.out_copy = out_copy;
+  a.esize = esize;
+  a.vec = aligned16(logits) && (row_stride * esize) % 16 == 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (dtype == MVLLM_DTYPE_BF16)
+    hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, grid, dim3(kArgmaxThreads), 0, s, a);
+  else if (dtype == MVLLM_DTYPE_F16)
+    hipLaunchKernelGGL(argmax_rows_kernel<f16_t>, grid, dim3(kArgmaxThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(argmax_rows_kernel<float>, grid, dim3(kArgmaxThreads), 0, s, a);
+  MVLLM_LAUNCH_CHECK("argmax_rows_kernel");
   return MVLLM_OK;
 }

@@ -16,7 +16,7 @@ import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libmvllm_amd.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -53,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "mvllm_add_rms_norm",
     "mvllm_qk_norm_rope_kv_write",
     "mvllm_silu_mul",
+    "mvllm_embed_rms_norm",
+    "mvllm_argmax_rows",
     "mvllm_last_error",
     "mvllm_abi_version",
 )
@@ -202,11 +204,19 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mvllm_add_rms_norm.argtypes = [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int32, _ptr]
     lib.mvllm_add_rms_norm.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope_kv_write.argtypes = [
-        p(Tensor3), p(Tensor3), p(Tensor3), _ptr, _ptr, _ptr, _ptr, ctypes.c_float, _ptr, p(KVCache), _ptr, _ptr,
+        p(Tensor3), p(Tensor3), p(Tensor3), _ptr, _ptr, _ptr, _ptr, _ptr, _i64, ctypes.c_float, _ptr, p(KVCache),
+        _ptr, _ptr,
     ]
     lib.mvllm_qk_norm_rope_kv_write.restype = ctypes.c_int
     lib.mvllm_silu_mul.argtypes = [_ptr, _i64, _ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr]
     lib.mvllm_silu_mul.restype = ctypes.c_int
+    lib.mvllm_embed_rms_norm.argtypes = [
+        _ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _i64, ctypes.c_float, ctypes.c_int32,
+        _ptr,
+    ]
+    lib.mvllm_embed_rms_norm.restype = ctypes.c_int
+    lib.mvllm_argmax_rows.argtypes = [_ptr, _i64, _i64, _i64, ctypes.c_int32, _ptr, _ptr, _ptr]
+    lib.mvllm_argmax_rows.restype = ctypes.c_int
     lib.mvllm_last_error.argtypes = []
     lib.mvllm_last_error.restype = ctypes.c_char_p
     lib.mvllm_abi_version.argtypes = []

@@ -61,6 +61,7 @@ from micro_vllm_amd.attention.spec import FullAttentionSpec
 from micro_vllm_amd.harness.block_pool import BlockPool
 from micro_vllm_amd.harness.model import DecoderModel
 from micro_vllm_amd.harness.prefix_hash import BlockHashChain
+from micro_vllm_amd.layers import argmax_rows
 from micro_vllm_amd.worker.packing import (
     DeviceBlockRows,
     allocate_packed_batch,
@@ -183,6 +184,9 @@ class GenerationEngine:
             )
             for _ in range(c.num_hidden_layers)
         ]
+        if getattr(model, "fused_layers", False):
+            # Rotary rows for every position a request may reach.
+            model.build_rotary_table(max_model_len)
         self.pool = BlockPool(num_blocks)
         self.enable_prefix_cache = enable_prefix_cache
         self.cache_namespace = cache_namespace
@@ -422,7 +426,7 @@ class GenerationEngine:
         if rows.numel() == 0:
             return []
         logits = self.model.logits(hidden.index_select(0, rows))
-        return logits.argmax(dim=-1).tolist()
+        return argmax_rows(logits).tolist()
 
     def generate(self, requests: list[Request], progress_seconds: float | None = None) -> GenerationResult:
         """Run every request to completion. Synchronous mode times the
@@ -735,13 +739,14 @@ class DecodeGraphs:
         """The decode step on a bucket's buffers: logits and greedy token of every row."""
 
         model = self.engine.model
-        ids = buffers.input_ids
-        # Placeholder -(1 + r): the token sampled at row r of the previous step.
-        ids = torch.where(ids < 0, self.last_tokens.index_select(0, (-ids - 1).clamp(min=0)), ids)
-        hidden = model.forward(ids, buffers.positions, self.engine.kv_caches, buffers.group_metadata[0])
+        # Placeholder ids -(1 + r) stand for the token sampled at row r of
+        # the previous step (resolved inside the embedding lookup).
+        hidden = model.forward(
+            buffers.input_ids, buffers.positions, self.engine.kv_caches, buffers.group_metadata[0],
+            placeholder_tokens=self.last_tokens,
+        )
         logits = model.logits(hidden)
-        tokens = logits.argmax(dim=-1)
-        self.last_tokens[: tokens.numel()].copy_(tokens)
+        tokens = argmax_rows(logits, copy_into=self.last_tokens)
         return logits, tokens
 
     @torch.inference_mode()

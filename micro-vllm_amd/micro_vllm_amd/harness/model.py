@@ -11,7 +11,9 @@ Follows the reference models layer by layer (src/micro_vllm/models/qwen.py:
 * rotary embedding in float32 with the rotate-half convention
   (layers/rotary_embedding.py:14-52). Angles are computed with the same
   float32 operations from a per-model inverse-frequency table, once per
-  step for all layers instead of once per layer.
+  step for all layers instead of once per layer; with fused layers, once
+  per model for every position up to the engine's maximum length (the same
+  elementwise operations give the same values) and gathered by position.
 
 The q/k/v and gate/up projections are stored as single fused weights so that
 each is one GEMM; every output column is the same dot product as in the
@@ -21,8 +23,9 @@ no checkpoint to load).
 With ``fused_layers=True`` the elementwise steps run as the HIP library's
 fused kernels (`micro_vllm_amd.layers`): residual add + RMSNorm, q/k norm +
 rotary embedding + paged-cache write, SwiGLU, followed by attention over the
-cache (`hip_attention_over_cache`). The torch path stays the restatement the
-fused kernels are checked against.
+cache (`hip_attention_over_cache`), and the embedding lookup fused with the
+first input RMSNorm. The torch path stays the restatement the fused kernels
+are checked against.
 """
 
 from __future__ import annotations
@@ -160,6 +163,21 @@ class DecoderModel:
             self.lm_head = normal(c.vocab_size, c.hidden_size, std=lm_head_std or init_std)
         indices = torch.arange(0, c.head_dim, 2, dtype=torch.float32, device=self.device)
         self.inverse_frequencies = 1.0 / (c.rope_theta ** (indices / c.head_dim))
+        # cos/sin [positions, head_dim] for the fused path (build_rotary_table).
+        self.rotary_cos: torch.Tensor | None = None
+        self.rotary_sin: torch.Tensor | None = None
+
+    def build_rotary_table(self, num_positions: int) -> None:
+        """cos/sin of every position below ``num_positions`` (kept if the
+        table already covers them): the fused path then gathers rows by
+        position instead of computing a table each step."""
+
+        if self.rotary_cos is not None and self.rotary_cos.shape[0] >= num_positions:
+            return
+        positions = torch.arange(num_positions, dtype=torch.int64, device=self.device)
+        cosine, sine = self.rotary_tables(positions)
+        self.rotary_cos = cosine.reshape(num_positions, self.config.head_dim).contiguous()
+        self.rotary_sin = sine.reshape(num_positions, self.config.head_dim).contiguous()
 
     def parameter_count(self) -> int:
         tensors = [self.embed, self.final_norm, *(t for layer in self.layers for t in layer.values())]
@@ -180,11 +198,16 @@ class DecoderModel:
         positions: torch.Tensor,
         kv_caches: list[torch.Tensor],
         metadata: AttentionMetadata,
+        placeholder_tokens: torch.Tensor | None = None,
     ) -> torch.Tensor:
-        """Final hidden states [tokens, hidden] of the flattened batch."""
+        """Final hidden states [tokens, hidden] of the flattened batch. An
+        input id ``-(1 + r)`` stands for ``placeholder_tokens[r]``."""
 
         if self.fused_layers:
-            return self._forward_fused(input_ids, positions, kv_caches, metadata)
+            return self._forward_fused(input_ids, positions, kv_caches, metadata, placeholder_tokens)
+        if placeholder_tokens is not None:
+            index = (-input_ids - 1).clamp(min=0)
+            input_ids = torch.where(input_ids < 0, placeholder_tokens.index_select(0, index), input_ids)
         c = self.config
         eps = c.rms_norm_eps
         n = input_ids.shape[0]
@@ -217,6 +240,7 @@ class DecoderModel:
         positions: torch.Tensor,
         kv_caches: list[torch.Tensor],
         metadata: AttentionMetadata,
+        placeholder_tokens: torch.Tensor | None = None,
     ) -> torch.Tensor:
         from micro_vllm_amd import layers
         from micro_vllm_amd.attention.operators.mi355x_paged import AttentionPlan, hip_attention_over_cache
@@ -226,11 +250,16 @@ class DecoderModel:
         n = input_ids.shape[0]
         q_size = c.num_attention_heads * c.head_dim
         kv_size = c.num_key_value_heads * c.head_dim
-        cosine, sine = self.rotary_tables(positions)
-        cosine = cosine.reshape(n, c.head_dim).contiguous()
-        sine = sine.reshape(n, c.head_dim).contiguous()
-        residual = F.embedding(input_ids, self.embed)
-        x = layers.add_rms_norm(residual, self.layers[0]["input_norm"], eps)
+        if self.rotary_cos is not None:
+            cosine, sine, table_positions = self.rotary_cos, self.rotary_sin, positions
+        else:
+            cosine, sine = self.rotary_tables(positions)
+            cosine = cosine.reshape(n, c.head_dim).contiguous()
+            sine = sine.reshape(n, c.head_dim).contiguous()
+            table_positions = None
+        residual, x = layers.embed_rms_norm(
+            input_ids, self.embed, self.layers[0]["input_norm"], eps, last_tokens=placeholder_tokens
+        )
         # Every layer sees the same batch: its work lists are built once.
         plan = AttentionPlan(metadata, c.num_attention_heads, kv_caches[0])
         for i, (layer, cache) in enumerate(zip(self.layers, kv_caches)):
@@ -249,6 +278,7 @@ class DecoderModel:
                 eps,
                 cache,
                 metadata.slot_mapping,
+                positions=table_positions,
             )
             attention = hip_attention_over_cache(q, cache, metadata, plan=plan)
             x = layers.add_rms_norm(F.linear(attention.flatten(1), layer["o"]), layer["post_norm"], eps, residual)

@@ -181,3 +181,130 @@ def test_fused_ops_reject_unsupported_inputs(device):
         layers.add_rms_norm(x, torch.ones(64, device=device), 1e-6)  # float32
     with pytest.raises(ValueError):
         layers.silu_mul(torch.randn((4, 6), device=device, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq", [16, 5], ids=["16q8kv", "5q1kv"])
+@pytest.mark.parametrize("n", [23, 2100], ids=["per-pass", "whole-token"])
+def test_qk_norm_rope_with_a_position_table_equals_per_token_tables(device, dtype, hq, n):
+    """Rows gathered by position from one table give exactly what the same
+    rows passed per token give (both kernel forms); a position outside the
+    table rotates only its own token, to NaN."""
+
+    hkv, d, bs = (8 if hq == 16 else 1), 128, 16
+    nb = -(-n // bs) + 2
+    gen = torch.Generator(device=device).manual_seed(17 + n)
+    qkv = torch.randn((n, (hq + 2 * hkv) * d), generator=gen, device=device).to(dtype)
+    q = qkv[:, : hq * d].view(n, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].view(n, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].view(n, hkv, d)
+    qw = (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(dtype)
+    kw = (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(dtype)
+    table_rows = 3000
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32, device=device) / d))
+    angles = torch.outer(torch.arange(table_rows, device=device).float(), inv)
+    angles = torch.cat((angles, angles), dim=-1)
+    cos_table, sin_table = angles.cos().contiguous(), angles.sin().contiguous()
+    positions = torch.randint(0, table_rows, (n,), generator=gen, device=device)
+    positions[1] = positions[0]  # a repeated position
+    positions[2] = table_rows - 1
+    slots = torch.randperm(nb * bs, generator=torch.Generator().manual_seed(3))[:n].to(device)
+    slots[5] = -1
+
+    def run(cos, sin, pos):
+        cache = torch.full((2, nb, bs, hkv, d), float("nan"), dtype=dtype, device=device)
+        q_out = layers.qk_norm_rope_kv_write(q, k, v, qw, kw, cos, sin, 1e-6, cache, slots, positions=pos)
+        return q_out, cache
+
+    want_q, want_cache = run(cos_table[positions].contiguous(), sin_table[positions].contiguous(), None)
+    got_q, got_cache = run(cos_table, sin_table, positions)
+    assert torch.equal(got_q.view(torch.int16), want_q.view(torch.int16))
+    assert torch.equal(got_cache.view(torch.int16), want_cache.view(torch.int16))
+
+    # One token past the table: its q and k come out NaN, v and every other
+    # token are unchanged.
+    outside = positions.clone()
+    outside[7] = table_rows
+    cache = torch.full((2, nb, bs, hkv, d), float("nan"), dtype=dtype, device=device)
+    got_q = layers.qk_norm_rope_kv_write(q, k, v, qw, kw, cos_table, sin_table, 1e-6, cache, slots, positions=outside)
+    others = torch.arange(n, device=device) != 7
+    assert torch.isnan(got_q[7]).all()
+    assert torch.equal(got_q[others].view(torch.int16), want_q[others].view(torch.int16))
+    flat, want_flat = cache.view(2, -1, hkv, d), want_cache.view(2, -1, hkv, d)
+    assert torch.isnan(flat[0, slots[7]]).all()
+    assert torch.equal(flat[1, slots[7]], v[7])
+    keep = others & (slots >= 0)
+    assert torch.equal(flat[:, slots[keep]].view(torch.int16), want_flat[:, slots[keep]].view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim", [1024, 4096])
+def test_embed_rms_norm_equals_embedding_then_rms_norm(device, dtype, dim):
+    """The gathered rows are the embedding rows bit for bit (placeholders
+    resolved through last_tokens, out-of-vocabulary ids give zero rows), and
+    the normalised rows equal add_rms_norm of those rows bit for bit."""
+
+    vocab, n = 5000, 300
+    gen = torch.Generator(device=device).manual_seed(dim)
+    embedding = torch.randn((vocab, dim), generator=gen, device=device).to(dtype)
+    weight = (1 + 0.1 * torch.randn(dim, generator=gen, device=device)).to(dtype)
+    last = torch.randint(0, vocab, (64,), generator=gen, device=device)
+    ids = torch.randint(0, vocab, (n,), generator=gen, device=device)
+    ids[::7] = -1 - torch.arange(0, n, 7, device=device) % 64  # placeholders for last[r]
+    ids[5], ids[6] = vocab, -1 - 64  # outside the vocabulary / past last_tokens
+    residual, out = layers.embed_rms_norm(ids, embedding, weight, 1e-6, last_tokens=last)
+
+    resolved = torch.where(ids < 0, last[(-ids - 1).clamp(0, 63)], ids)
+    valid = (ids < vocab) & (ids >= -64)
+    want = torch.zeros((n, dim), dtype=dtype, device=device)
+    want[valid] = F.embedding(resolved[valid], embedding)
+    assert torch.equal(residual.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), layers.add_rms_norm(want, weight, 1e-6).view(torch.int16))
+    assert_norm_close(out[valid], rms_norm(want[valid], weight, 1e-6), dtype)
+    assert not out[~valid].any()
+
+    residual2, out2 = layers.embed_rms_norm(ids.clamp(0, vocab - 1), embedding, weight, 1e-6)
+    assert torch.equal(residual2, F.embedding(ids.clamp(0, vocab - 1), embedding))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(
+    ("rows", "cols", "pad"),
+    [(256, 151_936, 0), (3, 128_256, 0), (5, 1001, 7), (4, 3000, 5), (1, 7, 0)],
+    ids=["qwen3-vocab", "llama3-vocab", "vector-tail", "strided", "tiny"],
+)
+def test_argmax_rows_matches_torch_argmax(device, dtype, rows, cols, pad):
+    """Indices identical to torch.argmax(dim=-1): ties go to the first index,
+    NaN is the maximum (its first occurrence), -0 equals +0, rows of -inf
+    give index 0; rows strided past their length; the copy gets the same."""
+
+    gen = torch.Generator(device=device).manual_seed(cols + rows)
+    full = torch.randint(-40, 40, (rows, cols + pad), generator=gen, device=device).to(dtype) / 8
+    logits = full[:, :cols]
+    r = min(rows, 5)
+    if r > 1:
+        logits[1, cols // 3] = float("nan")
+        logits[1, cols // 2] = float("nan")
+        logits[1, 0] = float("inf")
+    if r > 2:
+        logits[2] = float("-inf")
+    if r > 3:
+        logits[3] = -0.0
+        logits[3, cols - 1] = 0.0
+    if r > 4:
+        logits[4] = 1.0  # every entry ties
+    copy = torch.full((rows + 3,), -7, dtype=torch.int64, device=device)
+    got = layers.argmax_rows(logits, copy_into=copy)
+    want = torch.argmax(logits, dim=-1)
+    assert torch.equal(got, want)
+    assert torch.equal(copy[:rows], want) and (copy[rows:] == -7).all()
+
+
+def test_argmax_rows_on_misaligned_rows(device):
+    """Rows that start off 16-byte alignment take the scalar loads."""
+
+    gen = torch.Generator(device=device).manual_seed(3)
+    base = torch.randn((6, 2003), generator=gen, device=device).to(torch.bfloat16)
+    logits = base[:, 1:]
+    assert logits.data_ptr() % 16 != 0
+    assert torch.equal(layers.argmax_rows(logits), torch.argmax(logits, dim=-1))
