@@ -217,12 +217,13 @@ __global__ __launch_bounds__(256) void decode_split_lds_kernel(AttnArgs a) {
 
 // Blocks [0, R * head_groups): merge split partials of multi-split
 // decode requests, kCombineHeads query heads per block, 32 lanes per head
-// (4 dims each).
+// (4 dims each). Up to CAP splits are merged from one round of loads (the
+// launch picks CAP >= the layout's split count when it is at most 32).
 // Blocks after that: zero tokens outside every request, kZeroTokens each.
 constexpr int kZeroTokens = 16;
 constexpr int kCombineHeads = 8;
 
-template <typename T>
+template <typename T, int CAP>
 __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t head_groups) {
   const int64_t R = a.num_requests;
   const int64_t combine_blocks = R * head_groups;
@@ -230,12 +231,23 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
     const int64_t first = a.qsl[0], last = a.qsl[R];
     const int64_t t0 = (blockIdx.x - combine_blocks) * kZeroTokens;
     const int64_t row = static_cast<int64_t>(a.num_q_heads) * a.head_dim;
+    // Contiguous, 16-byte aligned token rows (the usual output): 16-byte
+    // stores of zero bits (+0 in every dtype); otherwise element stores.
+    const bool vec = a.o_s2 == 1 && a.o_s1 == a.head_dim && (row * static_cast<int64_t>(sizeof(T))) % 16 == 0 &&
+                     (a.o_s0 * static_cast<int64_t>(sizeof(T))) % 16 == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0;
     for (int64_t t = t0; t < t0 + kZeroTokens && t < a.num_tokens; ++t) {
       if (t >= first && t < last) continue;
       T* op = static_cast<T*>(a.out) + t * a.o_s0;
-      for (int64_t i = threadIdx.x; i < row; i += blockDim.x) {
-        const int64_t hq = i / a.head_dim, d = i - hq * a.head_dim;
-        Elem<T>::store(op + hq * a.o_s1 + d * a.o_s2, 0.f);
+      if (vec) {
+        const int64_t chunks = row * static_cast<int64_t>(sizeof(T)) / 16;
+        for (int64_t i = threadIdx.x; i < chunks; i += blockDim.x)
+          reinterpret_cast<uint4*>(op)[i] = uint4{0u, 0u, 0u, 0u};
+      } else {
+        for (int64_t i = threadIdx.x; i < row; i += blockDim.x) {
+          const int64_t hq = i / a.head_dim, d = i - hq * a.head_dim;
+          Elem<T>::store(op + hq * a.o_s1 + d * a.o_s2, 0.f);
+        }
       }
     }
     return;
@@ -254,8 +266,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
     // Nothing visible: softmax over no keys is NaN in the reference.
     const uint32_t nan_bits = Elem<T>::to_bits(NAN);
     w[0] = w[1] = nan_bits | (nan_bits << 16);
-  } else if (ns <= 8) {
-    // Up to eight splits (the common case): every split's (max, sum) and
+  } else if (ns <= CAP) {
+    // Up to CAP splits (the common case): every split's (max, sum) and
     // accumulator slice are loaded at once, one round trip after the table.
     const int sub = threadIdx.x & 31;
     const int64_t first_item = r * a.max_splits * a.num_q_heads + hq;
@@ -263,9 +275,9 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
     float2 ml = make_float2(-INFINITY, 0.f);
     if (sub < cnt) ml = a.ws_ml[first_item + sub * a.num_q_heads];
     const float* accp = a.ws_acc + first_item * kDim + d0;
-    float4_t v[8];
+    float4_t v[CAP];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CAP; ++j) {
       const int k = j < cnt ? j : cnt - 1;  // indices past the last split re-read it, unused
       v[j] = *reinterpret_cast<const float4_t*>(accp + static_cast<int64_t>(k) * a.num_q_heads * kDim);
     }
@@ -280,7 +292,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
     for (int m = 16; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 32);
     float4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CAP; ++j) {
       const float wj = __shfl(wgt, j, 32);
       if (j < cnt) o += v[j] * wj;
     }
@@ -398,8 +410,12 @@ int launch_combine_t(const AttnArgs& a, hipStream_t s) {
   const int64_t blocks = a.num_requests * head_groups + (a.num_tokens + kZeroTokens - 1) / kZeroTokens;
   if (blocks > 0) {
     if (blocks > INT32_MAX) return fail(MVLLM_ERR_INVALID, "combine grid too large");
-    hipLaunchKernelGGL(decode_combine_kernel<T>, dim3(static_cast<unsigned>(blocks)),
-                       dim3(32 * kCombineHeads), 0, s, a, head_groups);
+    // Short splits on small batches give requests up to ~20 splits; they
+    // still merge in one round of loads.
+    const dim3 grid(static_cast<unsigned>(blocks)), block(32 * kCombineHeads);
+    if (a.max_splits <= 8) hipLaunchKernelGGL((decode_combine_kernel<T, 8>), grid, block, 0, s, a, head_groups);
+    else if (a.max_splits <= 16) hipLaunchKernelGGL((decode_combine_kernel<T, 16>), grid, block, 0, s, a, head_groups);
+    else hipLaunchKernelGGL((decode_combine_kernel<T, 32>), grid, block, 0, s, a, head_groups);
     MVLLM_LAUNCH_CHECK("decode_combine_kernel");
   }
   return MVLLM_OK;

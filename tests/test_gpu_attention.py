@@ -233,6 +233,25 @@ def test_decode_kernel_group_sizes_and_context_boundaries(device, dtype, hq, hkv
     run_and_check(q, k, v, cache, md, dtype)
 
 
+@pytest.mark.parametrize(
+    ("requests", "longest"),
+    [(128, 1024), (16, 1024), (4, 3000)],
+    ids=["9-splits", "17-splits", "48-splits"],
+)
+def test_decode_combine_of_many_splits(device, requests, longest):
+    """Split lengths follow the batch (about two items per CU, at least 64
+    tokens), so smaller batches split each request more finely: on 256 CUs
+    these batches reach 9, 17 and 48 splits per request, which the combine
+    merges from one round of loads (up to 16 and 32) or in passes."""
+
+    rng = np.random.default_rng(requests)
+    lengths = rng.integers(1, longest + 1, size=requests)
+    lengths[0] = longest
+    q, k, v, cache, md = build_case(device, torch.bfloat16, lengths.tolist(), [1] * requests, 16, 8, 128, 16,
+                                    seed=requests)
+    run_and_check(q, k, v, cache, md, torch.bfloat16)
+
+
 @pytest.mark.parametrize("bs", [1, 5, 8, 32, 64])
 def test_decode_kernel_other_block_sizes(device, bs):
     lengths = [1, 7, 33, 200, 777]
