@@ -15,7 +15,9 @@ Reported (one JSON line on stdout):
 * ``prefill``: the prefill kernel on the Llama-3-head mixed batch (8 chunks
   of 512 + 248 decodes): causal-visible FLOPs / its mean duration, against
   the 2.5 PFLOP/s bf16 peak (serial pass), and the mixed step's time with
-  the decode and prefill workgroups in one step kernel;
+  the decode and prefill workgroups in one step kernel, also as a fraction
+  of its floor max(step bytes / HBM peak, prefill FLOPs / bf16 peak)
+  (``prefill.mixed_step_roofline``);
   ``prefill.library`` times the same chunks through PyTorch-ROCm's flash
   attention (variable-length, one launch) and a square bf16 GEMM through
   hipBLASLt on the same GPU;
@@ -1065,6 +1067,16 @@ def main() -> int:
         record["mixed_step_ms"] = round(shipped["ms_per_step"], 5)
         record["mixed_step_ms_serial"] = round(serial["ms_per_step"], 5)
         record["decode_part_frac"] = round(decode_kernel_bytes(mixed) / (serial["decode_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        # The whole mixed step against its own floor: the larger of the
+        # step's algorithmic bytes at the HBM peak and its prefill FLOPs at
+        # the bf16 peak.
+        floor_ms = max(workloads.decode_bytes(mixed) / (HBM_PEAK_GBS * 1e9),
+                       workloads.prefill_flops(mixed) / (BF16_PEAK_TFLOPS * 1e12)) * 1e3
+        record["mixed_step_roofline"] = {
+            "bound": "hbm" if workloads.decode_bytes(mixed) / (HBM_PEAK_GBS * 1e9) >= workloads.prefill_flops(mixed) / (BF16_PEAK_TFLOPS * 1e12) else "mfma",
+            "floor_ms": round(floor_ms, 5),
+            "frac": round(floor_ms / shipped["ms_per_step"], 4),
+        }
         from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
 
         mixed_out = hip_paged_attention(mixed.query, mixed.key, mixed.value, mixed.cache, mixed.metadata)
