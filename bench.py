@@ -151,7 +151,7 @@ def measured_traffic(workload: str) -> int | None:
 
 def host_threads() -> int:
     """Host threads for the CPU baseline: every core this process may use,
-    capped by OMP_NUM_THREADS when it is set (the GPU box's CPU share)."""
+    capped by OMP_NUM_THREADS when it is set (this process's CPU share)."""
 
     try:
         cores = len(os.sched_getaffinity(0))
@@ -333,7 +333,7 @@ def small_mixed_record(hip: "HipEvents", device, steps: int = 200, warmup: int =
 
 
 def torch_gathered_attention(query, key, value, cache, md, scale: float):
-    """The operator's semantics in plain torch, as a same-box GPU baseline.
+    """The operator's semantics in plain torch, as a baseline on the same GPU.
 
     Writes K/V into the cache (``index_copy_`` on the flat slot view, padded
     slots skipped), then per request gathers the keys of
@@ -912,7 +912,7 @@ def main() -> int:
         "--no-llama3-e2e", action="store_true", help="skip the Llama-3-8B end-to-end run of the default workload"
     )
     parser.add_argument(
-        "--no-torch-baseline", action="store_true", help="skip the same-box torch gathered-attention baseline"
+        "--no-torch-baseline", action="store_true", help="skip the torch gathered-attention baseline on the same GPU"
     )
     parser.add_argument(
         "--copy-calibration-mib",

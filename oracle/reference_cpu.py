@@ -1,6 +1,6 @@
 """The reference operator's CPU path in torch (TEST INFRASTRUCTURE ONLY).
 
-The CPU baseline that ``bench.py`` times on the GPU box's host cores, and
+The CPU baseline that ``bench.py`` times on the GPU host's own cores, and
 nothing else: the HIP library never calls it. It performs the same steps as
 ``ReferenceAttentionOperator.forward`` (src/micro_vllm/attention/operators/
 reference.py:14-81, with ``write_kv_cache`` :84-98 and ``gather_kv_cache``
