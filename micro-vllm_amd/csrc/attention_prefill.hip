@@ -154,11 +154,6 @@ __device__ __forceinline__ float sum_with_partner(float x) {
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4v;
 
-// Transposing LDS read (see the file comment for its lane layout).
-__device__ __forceinline__ short4v lds_read_tr16(const uint8_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(p));
-}
-
 // lds_dma_load16_sbase with the LDS destination given as a wave-uniform
 // base plus an immediate, added straight into M0 (s_add_u32 also writes SCC,
 // which the clobber list declares).

@@ -125,10 +125,6 @@ template <> struct Elem<f16_t> {
 
 // ------------------------------------------------------- wave utilities ----
 
-__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
-}
-
 // Lane exchanges across 16- and 32-lane halves in one VALU instruction each
 // (gfx950 v_permlane16_swap / v_permlane32_swap with both operands x): the
 // two results hold x of this lane and of lane ^ 16 (^ 32), in an order that

@@ -75,9 +75,6 @@ class DeviceBlockRows:
             self._slot_of[request_id] = slot
         return slot
 
-    def has_slot(self, request_id: str) -> bool:
-        return request_id in self._slot_of
-
     def release(self, request_id: str) -> None:
         slot = self._slot_of.pop(request_id, None)
         if slot is not None:
