@@ -808,6 +808,22 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
     return out
 
 
+def step_roofline(w, step_ms: float) -> dict:
+    """A step against its own floor: the larger of its algorithmic bytes at
+    the HBM peak and its prefill FLOPs at the bf16 peak, over its time."""
+
+    from micro_vllm_amd import workloads
+
+    hbm_ms = workloads.decode_bytes(w) / (HBM_PEAK_GBS * 1e9) * 1e3
+    mfma_ms = workloads.prefill_flops(w) / (BF16_PEAK_TFLOPS * 1e12) * 1e3
+    floor_ms = max(hbm_ms, mfma_ms)
+    return {
+        "bound": "hbm" if hbm_ms >= mfma_ms else "mfma",
+        "floor_ms": round(floor_ms, 5),
+        "frac": round(floor_ms / step_ms, 4),
+    }
+
+
 def prefill_record(w, timing: dict) -> dict:
     from micro_vllm_amd import workloads
 
@@ -1067,16 +1083,7 @@ def main() -> int:
         record["mixed_step_ms"] = round(shipped["ms_per_step"], 5)
         record["mixed_step_ms_serial"] = round(serial["ms_per_step"], 5)
         record["decode_part_frac"] = round(decode_kernel_bytes(mixed) / (serial["decode_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-        # The whole mixed step against its own floor: the larger of the
-        # step's algorithmic bytes at the HBM peak and its prefill FLOPs at
-        # the bf16 peak.
-        floor_ms = max(workloads.decode_bytes(mixed) / (HBM_PEAK_GBS * 1e9),
-                       workloads.prefill_flops(mixed) / (BF16_PEAK_TFLOPS * 1e12)) * 1e3
-        record["mixed_step_roofline"] = {
-            "bound": "hbm" if workloads.decode_bytes(mixed) / (HBM_PEAK_GBS * 1e9) >= workloads.prefill_flops(mixed) / (BF16_PEAK_TFLOPS * 1e12) else "mfma",
-            "floor_ms": round(floor_ms, 5),
-            "frac": round(floor_ms / shipped["ms_per_step"], 4),
-        }
+        record["mixed_step_roofline"] = step_roofline(mixed, shipped["ms_per_step"])
         from micro_vllm_amd.attention.operators.mi355x_paged import hip_paged_attention
 
         mixed_out = hip_paged_attention(mixed.query, mixed.key, mixed.value, mixed.cache, mixed.metadata)

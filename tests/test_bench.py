@@ -41,6 +41,32 @@ def test_decode_kernel_bytes_counts_every_visible_row_once():
     assert bench.decode_kernel_bytes(w) == kv + qo + table + meta
 
 
+def test_step_roofline_takes_the_larger_floor():
+    # One decode of 1,000 tokens and one 100-token prefill chunk at offset
+    # 400: 2 KV heads x 4 dims in bf16, 4 query heads, block 16.
+    w = SimpleNamespace(
+        query=SimpleNamespace(element_size=lambda: 2),
+        context_lengths=np.array([1000, 500]),
+        query_lengths=np.array([1, 100]),
+        num_kv_heads=2,
+        num_q_heads=4,
+        head_dim=4,
+        block_size=16,
+    )
+    sys.path.insert(0, str(ROOT / "micro-vllm_amd"))
+    from micro_vllm_amd import workloads
+
+    flops = 4 * 4 * 4 * (100 * 400 + 100 * 101 // 2)
+    assert workloads.prefill_flops(w) == flops
+    step_bytes = workloads.decode_bytes(w)
+    hbm_ms = step_bytes / 8e12 * 1e3
+    mfma_ms = flops / 2.5e15 * 1e3
+    r = bench.step_roofline(w, 2 * max(hbm_ms, mfma_ms))
+    assert r["bound"] == ("hbm" if hbm_ms >= mfma_ms else "mfma")
+    assert abs(r["floor_ms"] - max(hbm_ms, mfma_ms)) < 1e-5
+    assert r["frac"] == 0.5
+
+
 def test_more_than_one_gpu_is_refused_with_a_message():
     result = subprocess.run(
         [sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],

@@ -116,7 +116,7 @@ def check_against_reference(requests, hip_model, ref_model, device, group=None):
     return checked
 
 
-def models(device, seed=3, fused_layers=False, copy_head=True, **overrides):
+def models(device, seed=3, fused_layers=False, copy_head=True, dtype=torch.bfloat16, **overrides):
     """The HIP model and the reference-semantics model on the same weights."""
 
     base = overrides.pop("base", DecoderConfig.qwen3_0_6b)
@@ -124,7 +124,8 @@ def models(device, seed=3, fused_layers=False, copy_head=True, **overrides):
     overrides.setdefault("vocab_size", VOCAB)
     cfg = base(**overrides)
     hip_model = DecoderModel(
-        cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed, fused_layers=fused_layers
+        cfg, get_attention_operator_class("mi355x_paged")(), device=device, seed=seed, fused_layers=fused_layers,
+        dtype=dtype,
     )
     if copy_head:
         make_copy_model(hip_model, offset=COPY_OFFSET)
@@ -169,6 +170,21 @@ def test_fused_layer_kernels_match_reference_decoding(device, qk_norm):
 
     hip_model, ref_model = models(device, seed=9, fused_layers=True, qk_norm=qk_norm)
     requests = make_requests(seed=6, count=7, lo=40, hi=160, max_tokens=12)
+    engine = GenerationEngine(
+        hip_model, num_blocks=256, max_num_batched_tokens=200, max_num_seqs=8, max_model_len=512, decode_graphs=True
+    )
+    result = engine.generate(requests)
+    assert result.output_tokens == 7 * 12
+    check_against_reference(requests, hip_model, ref_model, device)
+
+
+def test_fused_layer_kernels_match_reference_decoding_in_fp16(device):
+    """The same in float16: the fused layer kernels, the embedding lookup, the
+    decode graphs with the fp16 attention kernels and the argmax, against the
+    torch layers and the reference-semantics operator in float16."""
+
+    hip_model, ref_model = models(device, seed=12, fused_layers=True, dtype=torch.float16)
+    requests = make_requests(seed=8, count=7, lo=40, hi=160, max_tokens=12)
     engine = GenerationEngine(
         hip_model, num_blocks=256, max_num_batched_tokens=200, max_num_seqs=8, max_model_len=512, decode_graphs=True
     )
