@@ -31,10 +31,18 @@
 // The online softmax (FlashAttention-2, Dao 2023) runs in the exp2 domain and
 // rescales the accumulators only when a row's maximum grows by more than 2^8
 // (lazy rescaling as in FlashAttention-3, Shah et al. 2024); the final
-// normalisation divides by a sum taken with the same offsets. In bf16, halves
-// that need no masking first skip the row maximum: their probabilities are
-// taken against the current offset, and the half is redone from its maximum
-// only if some lane's sum exceeds 2^12 (or is not finite).
+// normalisation divides by a sum taken with the same offsets. Q is multiplied
+// once per item by the softmax scale in the exp2 domain (log2(e) / sqrt(D))
+// and rounded back to the input type, and the S MFMA chain starts from the
+// row's running offset negated, so the MFMAs produce scaled, offset scores
+// and an unmasked half takes exp2 of them directly. In bf16, halves that need
+// no masking first skip the row maximum: their probabilities are taken
+// against the current offset, and the half is redone from its maximum only
+// if some lane's sum exceeds 2^12 (or is not finite).
+//
+// Order inside a tile: S(0); softmax(0); S(1); softmax(1) and P.V(0) in one
+// basic block, which the compiler interleaves (the vector work of one half
+// beside the other half's MFMAs); P.V(1); the tile's barrier.
 //
 // Masking: scores are masked only on tiles that cross a row's visible range
 // or hold an unmapped page. V rows outside the workgroup's visible key range
