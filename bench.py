@@ -7,6 +7,11 @@ the Qwen3-0.6B-head decode batch: 256 sequences, contexts U[128, 4096]
 (seed 0), 16 query / 8 KV heads, head_dim 128, block 16, bf16, blocks drawn
 from a shuffled 70,000-block pool, values N(0,1)*0.5.
 
+Each timed measurement first runs untimed forwards for ``--settle-ms`` of wall
+time, then its ``--warmup`` untimed steps, then ``--steps`` timed ones: a GPU
+that was idle runs its first ~50 back-to-back forwards up to 3-4% slower
+while its clock ramps (``settle`` in the line records how many ran).
+
 Reported (one JSON line on stdout):
 * ``value``: algorithmic HBM bytes of the step / step time, in GB/s;
 * ``roofline``: the decode kernel's algorithmic bytes per launch / its mean
@@ -41,7 +46,7 @@ Reported (one JSON line on stdout):
 * ``cpu_baseline``: the reference operator's CPU path (torch, bf16 cache,
   fp32 math, every available host core) on the same batch.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload qwen3_decode] [--quick]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--settle-ms 150] [--workload qwen3_decode] [--quick]
 
 Other workloads: ``llama3_mixed``, ``llama3_long_decode``, ``llama3_long_prefill``
 (8 chunks of 512 at offsets U[14336, 16384]), ``llama3_causal_prefill`` (8
@@ -700,7 +705,27 @@ def attention_workload(name: str, device):
     )
 
 
-def time_kv_write(w, hip: HipEvents, device, steps: int, warmup: int) -> dict:
+def settle(run, settle_ms: float) -> int:
+    """Untimed forwards for ``settle_ms`` of wall time (synchronized every 8)
+    before a measurement's warm-up steps: a GPU that was idle runs its first
+    ~50 back-to-back forwards up to 3-4% slower while its clock ramps, and
+    five warm-up steps leave the timed ones inside that ramp. Returns the
+    number of forwards run."""
+
+    import torch
+
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        run()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
+def time_kv_write(w, hip: HipEvents, device, steps: int, warmup: int, settle_ms: float = 0.0) -> dict:
     """The KV-cache write on its own (``mvllm_kv_write``: one launch of
     ``kv_write_rows_kernel``) over the batch's tokens, timed between HIP events
     on the launch stream. The shipped forward fuses this copy into its
@@ -713,6 +738,7 @@ def time_kv_write(w, hip: HipEvents, device, steps: int, warmup: int) -> dict:
     events = hip.create(2 * steps)
     stream = torch.cuda.current_stream(device).cuda_stream
     hip.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    settle(lambda: hip_write_kv_cache(w.key, w.value, w.cache, w.metadata), settle_ms)
     for _ in range(warmup):
         hip_write_kv_cache(w.key, w.value, w.cache, w.metadata)
     torch.cuda.synchronize()
@@ -740,8 +766,11 @@ def time_kv_write(w, hip: HipEvents, device, steps: int, warmup: int) -> dict:
     }
 
 
-def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurrent: bool = True) -> dict:
-    """``warmup`` untimed forwards, then ``steps`` timed ones between HIP
+def time_attention(
+    w, hip: HipEvents, device, steps: int, warmup: int, concurrent: bool = True, settle_ms: float = 0.0
+) -> dict:
+    """``settle_ms`` of untimed forwards (``settle``) and ``warmup`` untimed
+    forwards, then ``steps`` timed ones between HIP
     events on the launch stream. ``concurrent`` True times the shipped step:
     for a batch with prefill work that is the one-launch step kernel (decode
     and prefill workgroups in one grid), and the library's decode events
@@ -776,6 +805,7 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
         return hip_paged_attention(w.query, w.key, w.value, w.cache, w.metadata, timing=timing)
 
     try:
+        settled = settle(lambda: step(None), settle_ms)
         for _ in range(warmup):
             step(None)
         torch.cuda.synchronize()
@@ -785,6 +815,7 @@ def time_attention(w, hip: HipEvents, device, steps: int, warmup: int, concurren
         hip.hip.hipEventRecord(ctypes.c_void_p(marks[1]), ctypes.c_void_p(stream))
         torch.cuda.synchronize()
         out = {
+            "settle_forwards": settled,
             "ms_per_step": hip.elapsed_ms(marks[0], marks[1]) / steps,
             "decode_ms": statistics.mean(hip.elapsed_ms(decode_events[2 * i], decode_events[2 * i + 1]) for i in range(steps)),
         }
@@ -883,6 +914,12 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument(
+        "--settle-ms",
+        type=float,
+        default=150.0,
+        help="untimed forwards for this long before each measurement's warm-up steps (0: none)",
+    )
+    parser.add_argument(
         "--workload",
         default="qwen3_decode",
         choices=[
@@ -968,7 +1005,7 @@ def main() -> int:
         description += "; metadata without the max_query_len hint"
     torch.cuda.synchronize()
     hip = HipEvents()
-    timing = time_attention(w, hip, device, args.steps, args.warmup)
+    timing = time_attention(w, hip, device, args.steps, args.warmup, settle_ms=args.settle_ms)
     ms_per_step, decode_ms = timing["ms_per_step"], timing["decode_ms"]
     overlap = None
     if args.workload in PREFILL_WORKLOADS:
@@ -976,7 +1013,7 @@ def main() -> int:
         # decode and the prefill workgroups. The step above is that shipped
         # one; each kernel's roofline comes from a second pass with the two
         # kernels launched separately, one after the other.
-        serial = time_attention(w, hip, device, args.steps, args.warmup, concurrent=False)
+        serial = time_attention(w, hip, device, args.steps, args.warmup, concurrent=False, settle_ms=args.settle_ms)
         decode_ms = serial["decode_ms"]
         overlap = {
             "ms_per_step_serial": round(serial["ms_per_step"], 5),
@@ -994,6 +1031,12 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {
+            "ms": args.settle_ms,
+            "forwards": timing["settle_forwards"],
+            "note": "untimed forwards before the warm-up steps, so that the timed steps run at the clock the "
+            "part settles at under this load",
+        },
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -1076,8 +1119,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         result["config1"] = small_mixed_record(hip, device)
         mixed, mixed_description = attention_workload("llama3_mixed", device)
-        shipped = time_attention(mixed, hip, device, args.steps, args.warmup)
-        serial = time_attention(mixed, hip, device, args.steps, args.warmup, concurrent=False)
+        shipped = time_attention(mixed, hip, device, args.steps, args.warmup, settle_ms=args.settle_ms)
+        serial = time_attention(mixed, hip, device, args.steps, args.warmup, concurrent=False, settle_ms=args.settle_ms)
         record = prefill_record(mixed, serial)
         record["workload"] = mixed_description
         record["mixed_step_ms"] = round(shipped["ms_per_step"], 5)
@@ -1092,7 +1135,7 @@ def main() -> int:
         if not args.no_cpu_baseline:
             record["cpu_baseline"] = cpu_prefill_baseline(mixed)
         result["prefill"] = record
-        kv = time_kv_write(mixed, hip, device, args.steps, args.warmup)
+        kv = time_kv_write(mixed, hip, device, args.steps, args.warmup, settle_ms=args.settle_ms)
         kv["workload"] = f"llama3_mixed: the step's {kv['tokens']:,} tokens (8 KV heads, head_dim 128, bf16)"
         result["kv_write"] = kv
         del mixed
