@@ -102,7 +102,9 @@ typedef struct mvllm_batch {
   int64_t block_size;
   int64_t max_query_len; /* largest query count of a request, if the caller
                             knows it (<= 0: unknown). 1 lets a decode-only
-                            batch skip the prefill launch. */
+                            batch skip the prefill launch; the rows of any
+                            request with another query count then come back
+                            NaN. */
 } mvllm_batch;
 
 /*

@@ -66,6 +66,9 @@ struct AttnArgs {
   // the workspace (planned once for a step), so the launches skip the
   // work-list kernels.
   int32_t lists_ready;
+  // The caller's max_query_len hint said 1 (no prefill launch): the combine
+  // kernel makes the rows of any request with another query count NaN.
+  int32_t decode_only;
 };
 
 // Visible key positions [lo, hi] of query `t` in request `r` whose first

@@ -284,6 +284,7 @@ int bind_workspace(AttnArgs& a, const mvllm_batch* batch, int64_t Hq, int64_t D,
   char* const w = static_cast<char*>(workspace);
   a.split_tokens = d.split_tokens;
   a.max_splits = d.max_splits;
+  a.decode_only = batch->max_query_len == 1 ? 1 : 0;
   a.ws_acc = reinterpret_cast<float*>(w);
   a.ws_ml = reinterpret_cast<float2*>(w + d.acc_bytes);
   a.items = reinterpret_cast<PrefillItem*>(w + d.acc_bytes + d.ml_bytes);

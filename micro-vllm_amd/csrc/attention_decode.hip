@@ -259,8 +259,22 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(AttnArgs a, int32_t
   // request, and a single split has written its output itself.
   const int2 req = a.decode_req[r];
   const int64_t qs = req.x, ns = req.y;
-  if (ns < 0 || ns == 1 || ns > a.max_splits || qs < 0 || qs >= a.num_tokens) return;
   const int d0 = (threadIdx.x & 31) * 4;
+  if (ns < 0 && a.decode_only) {
+    // A request with another query count in a batch whose hint promised
+    // single-query requests only: no kernel computes its rows, so they are
+    // made NaN rather than left holding whatever the output memory held.
+    const int64_t q0 = a.qsl[r], q1 = a.qsl[r + 1];
+    if (q0 < 0 || q1 > a.num_tokens) return;
+    const uint32_t nan_bits = Elem<T>::to_bits(NAN);
+    const uint32_t nan2 = nan_bits | (nan_bits << 16);
+    for (int64_t t = q0; t < q1; ++t) {
+      uint16_t* op = static_cast<uint16_t*>(a.out) + t * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1;
+      *reinterpret_cast<uint2*>(op + d0) = uint2{nan2, nan2};
+    }
+    return;
+  }
+  if (ns < 0 || ns == 1 || ns > a.max_splits || qs < 0 || qs >= a.num_tokens) return;
   uint32_t w[2];
   if (ns == 0) {
     // Nothing visible: softmax over no keys is NaN in the reference.

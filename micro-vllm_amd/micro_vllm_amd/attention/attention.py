@@ -29,7 +29,8 @@ class AttentionMetadata:
     block_size: int
     # Optional host-side hint (not in the reference's metadata): the largest
     # number of queries of any request. Packing knows it without a device
-    # read; 1 lets a decode-only batch skip the prefill launch.
+    # read; 1 lets a decode-only batch skip the prefill launch (a request
+    # with more queries then gets NaN rows).
     max_query_len: int | None = None
 
     @property

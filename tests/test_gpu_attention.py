@@ -522,6 +522,23 @@ def test_step_kernel_on_a_decode_only_batch_without_the_hint(device, monkeypatch
     assert torch.equal(unhinted.view(torch.int16), hinted.view(torch.int16))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wrong_decode_only_hint_leaves_nan_rows_not_stale_memory(device, dtype):
+    """A hint of max_query_len = 1 skips the prefill launch. If a request
+    has more queries anyway, its rows come back NaN (not whatever the output
+    memory held); the decode rows and the cache write stay correct."""
+
+    lengths, qlens = [40, 300, 17, 2500], [5, 1, 1, 1]
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, 16, 8, 128, 16, seed=95)
+    before = cache.clone()
+    out = operator()(q, k, v, cache, dataclasses.replace(md, max_query_len=1))
+    torch.cuda.synchronize()
+    expected_cache, expected = oracle_step(q, k, v, before, md)
+    assert_cache_bit_exact(cache, expected_cache)
+    assert torch.isnan(out[:5].float()).all()
+    assert_attention_close(out[5:], expected[5:], **TOL[dtype])
+
+
 def test_plan_for_other_metadata_is_rejected(device):
     from micro_vllm_amd.attention.operators.mi355x_paged import AttentionPlan, hip_attention_over_cache
 
