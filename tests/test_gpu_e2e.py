@@ -51,38 +51,59 @@ def make_requests(seed, count, lo, hi, max_tokens, vocab=VOCAB):
 
 
 @torch.inference_mode()
-def teacher_forced_logits(model, sequences, device, last=None):
+def teacher_forced_logits(model, sequences, device, last=None, chunk=None):
     """Logits of every position of each sequence (one prefill step); with
-    ``last`` only those of each sequence's last ``last[i]`` positions."""
+    ``last`` only those of each sequence's last ``last[i]`` positions. With
+    ``chunk``, the sequences are prefilled ``chunk`` tokens at a time over
+    the same caches (chunked prefill), which bounds the reference
+    attention's score matrices on long sequences."""
 
-    plan_items, block, tables = [], 0, []
-    for i, seq in enumerate(sequences):
+    tables, block = [], 0
+    for seq in sequences:
         nb = -(-len(seq) // 16)
         tables.append(tuple(range(block, block + nb)))
         block += nb
-        plan_items.append(
-            ScheduledRequest(f"s{i}", tuple(seq), 0, len(seq), True, (CacheGroupBlockTable(tables[-1]),))
-        )
     caches = [
         torch.zeros((2, block + 1, 16, model.config.num_key_value_heads, 128), dtype=model.dtype, device=device)
         for _ in range(model.config.num_hidden_layers)
     ]
-    packed = pack_scheduler_output(
-        SchedulerOutput(tuple(plan_items)), specs=[FullAttentionSpec()], block_size=16, null_block_id=block, device=device
-    )
-    hidden = model.forward(packed.input_ids, packed.positions, caches, packed.group_metadata[0])
+    last = last if last is not None else [len(seq) for seq in sequences]
+    longest = max(len(seq) for seq in sequences)
+    step = chunk or longest
+    kept = [[] for _ in sequences]
+    for c0 in range(0, longest, step):
+        plan_items, spans = [], []
+        for i, seq in enumerate(sequences):
+            if c0 >= len(seq):
+                continue
+            n = min(step, len(seq) - c0)
+            plan_items.append(
+                ScheduledRequest(f"s{i}", tuple(seq[c0 : c0 + n]), c0, n, True, (CacheGroupBlockTable(tables[i]),))
+            )
+            spans.append((i, c0, n))
+        packed = pack_scheduler_output(
+            SchedulerOutput(tuple(plan_items)), specs=[FullAttentionSpec()], block_size=16, null_block_id=block,
+            device=device,
+        )
+        hidden = model.forward(packed.input_ids, packed.positions, caches, packed.group_metadata[0])
+        offset = 0
+        for i, p0, n in spans:
+            first = len(sequences[i]) - last[i]
+            lo, hi = max(first, p0), p0 + n
+            if hi > lo:
+                kept[i].append(hidden[offset + lo - p0 : offset + hi - p0])
+            offset += n
+        del hidden
     del caches
-    if last is not None:
-        ends = np.cumsum([len(seq) for seq in sequences])
-        rows = np.concatenate([np.arange(e - k, e) for e, k in zip(ends, last)])
-        hidden = hidden.index_select(0, torch.as_tensor(rows, device=hidden.device))
+    hidden = torch.cat([h for rows in kept for h in rows])
     return model.logits(hidden).float()
 
 
-def check_against_reference(requests, hip_model, ref_model, device, group=None):
+def check_against_reference(requests, hip_model, ref_model, device, group=None, chunk=None):
     """Teacher-forced check of every generated position (see module doc):
     identical greedy tokens, on a margin the test verifies. ``group`` bounds
-    how many sequences are teacher-forced in one step."""
+    how many sequences are teacher-forced in one step, ``chunk`` how many
+    tokens of each are prefilled at a time."""
 
     group = group or len(requests)
     max_diff = 0.0
@@ -91,8 +112,8 @@ def check_against_reference(requests, hip_model, ref_model, device, group=None):
         part = requests[g0 : g0 + group]
         sequences = [r.prompt_token_ids + r.output_token_ids[:-1] for r in part]
         last = [len(r.output_token_ids) for r in part]
-        ref_logits = teacher_forced_logits(ref_model, sequences, device, last)
-        hip_logits = teacher_forced_logits(hip_model, sequences, device, last)
+        ref_logits = teacher_forced_logits(ref_model, sequences, device, last, chunk)
+        hip_logits = teacher_forced_logits(hip_model, sequences, device, last, chunk)
         assert torch.isfinite(hip_logits).all()
         max_diff = max(max_diff, (hip_logits - ref_logits).abs().max().item())
         offset = 0
@@ -444,6 +465,47 @@ def test_llama3_shared_prefix_with_preemption_greedy_tokens_match_reference(devi
     assert result.preemptions > 0
     assert result.prefix_hit_tokens >= (5 + result.preemptions) * 4096
     assert check_against_reference(requests, hip_model, ref_model, device) == 6 * 64
+
+
+def test_llama3_config5_context_lengths_greedy_tokens_match_reference(device):
+    """The Llama-3-8B end-to-end configuration at its own context lengths:
+    the Llama-3-8B layer shape (hidden 4096, 32/8 heads of 128, MLP 14,336,
+    vocab 128,256), 4 layers; four requests share a 4,096-token random
+    prefix, each followed by its own suffix drawn from U[4096, 28672] with the
+    longest forced to 28,672, so contexts reach 32,784 tokens. Prefix cache
+    on, max_num_batched_tokens 8,192 (every prompt is chunked), HIP-graph
+    decode steps with the host one step ahead; 16 greedy tokens per request,
+    each equal to the reference-semantics operator's, teacher-forced in
+    prefill chunks of 4,096."""
+
+    hip_model, ref_model = models(
+        device, seed=35, fused_layers=True, base=DecoderConfig.llama3_8b, num_hidden_layers=4, vocab_size=LLAMA3_VOCAB
+    )
+    rng = np.random.default_rng(35)
+    prefix = rng.integers(0, LLAMA3_VOCAB, size=4096).tolist()
+    suffixes = [28672] + [int(x) for x in rng.integers(4096, 28673, size=3)]
+    requests = [
+        Request(f"r{i}", prefix + rng.integers(0, LLAMA3_VOCAB, size=n).tolist(), 16) for i, n in enumerate(suffixes)
+    ]
+    blocks_per_request = -(-(4096 + max(suffixes) + 16) // 16)
+    engine = GenerationEngine(
+        hip_model,
+        num_blocks=4 * blocks_per_request + 64,
+        max_num_batched_tokens=8192,
+        max_num_seqs=4,
+        max_model_len=blocks_per_request * 16,
+        decode_graphs=True,
+        pipeline=True,
+        enable_prefix_cache=True,
+        cache_namespace="llama3-config5",
+    )
+    result = engine.generate(requests)
+    print(f"steps {result.steps}, prefix-cache hit tokens {result.prefix_hit_tokens}, suffixes {suffixes}")
+    assert result.output_tokens == 4 * 16
+    assert result.prefix_hit_tokens >= 3 * 4096
+    del engine
+    torch.cuda.empty_cache()
+    assert check_against_reference(requests, hip_model, ref_model, device, group=1, chunk=4096) == 4 * 16
 
 
 def test_duplicate_prompts_share_canonical_blocks_through_the_device_block_table(device):
