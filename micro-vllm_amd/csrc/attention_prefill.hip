@@ -35,8 +35,8 @@
 // once per item by the softmax scale in the exp2 domain (log2(e) / sqrt(D))
 // and rounded back to the input type, and the S MFMA chain starts from the
 // row's running offset negated, so the MFMAs produce scaled, offset scores
-// and an unmasked half takes exp2 of them directly. In bf16, halves that need
-// no masking first skip the row maximum: their probabilities are taken
+// and an unmasked half takes exp2 of them directly. Halves that need no
+// masking first skip the row maximum: their probabilities are taken
 // against the current offset, and the half is redone from its maximum only
 // if some lane's sum exceeds 2^12 (or is not finite).
 //
@@ -107,6 +107,11 @@ template <> struct Mma32<f16_t> {
   }
   __device__ static float2v unpack2(uint32_t w) {
     return __builtin_convertvector(__builtin_bit_cast(f16x2_t, w), float2v);
+  }
+  // acc + the two fp16 values of w.
+  __device__ static float dot2_ones(uint32_t w, float acc) {
+    const f16x2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
   }
 };
 
@@ -229,7 +234,7 @@ __device__ __forceinline__ void fill_tile_record(int32_t* tbl, const AttnArgs& a
   rec[1] = int4{e[2], static_cast<int32_t>(mask), e[3], static_cast<int32_t>(mask)};
 }
 
-template <typename T, bool PSPLIT>
+template <typename T>
 __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, uint8_t* smem, uint32_t wg) {
   uint8_t* const kbuf = smem;                   // K stages 0, 1 (16 KiB each)
   uint8_t* const vbuf = smem + 2 * kTileBytes;  // V stages 0, 1
@@ -541,7 +546,7 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         }
       };
       // O^T += V^T . P^T over a half's two 16-key steps.
-      auto pv_mma = [&](const short4v (&vf)[2][8], const short8_t (&pb)[2], const short8_t (&pbl)[2]) {
+      auto pv_mma = [&](const short4v (&vf)[2][8], const short8_t (&pb)[2]) {
 #pragma unroll
         for (int q = 0; q < 2; ++q)
 #pragma unroll
@@ -549,43 +554,36 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
             const short4v lo4 = vf[q][c], hi4 = vf[q][4 + c];
             const short8_t av = short8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
             oacc[c] = Mma32<T>::mma(av, pb[q], oacc[c]);
-            if constexpr (PSPLIT) oacc[c] = Mma32<T>::mma(av, pbl[q], oacc[c]);
           }
       };
-      // Probabilities exp2(s + shift) (P^T B operands in pb/pbl), the add
+      // Probabilities exp2(s + shift) (P^T B operands in pb), the add
       // skipped for SHIFTED false; returns this lane's share of their row
-      // sum (bf16: the rounded values).
-      auto make_p = [&](const float16v& s, float shift, auto shifted_c, short8_t (&pb)[2], short8_t (&pbl)[2]) {
+      // sum, taken over the rounded values the P.V product uses.
+      auto make_p = [&](const float16v& s, float shift, auto shifted_c, short8_t (&pb)[2]) {
         constexpr bool SHIFTED = decltype(shifted_c)::value;
         float inc = 0.f;
         float p[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           p[i] = __builtin_amdgcn_exp2f(SHIFTED ? s[i] + shift : s[i]);
-          if constexpr (PSPLIT) inc += p[i];
         }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           // P^T B operand: keys 16 s2 + 8 u + 4 hh + e  <->  k = 8 hh + 4 u + e.
-          uint32_t ph[4], pl[4];
+          uint32_t ph[4];
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             ph[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w], p[8 * s2 + 2 * w + 1]);
-            if constexpr (!PSPLIT) inc = Mma32<T>::dot2_ones(ph[w], inc);
-            if constexpr (PSPLIT) {
-              const float2v back = Mma32<T>::unpack2(ph[w]);
-              pl[w] = Mma32<T>::pack2(p[8 * s2 + 2 * w] - back[0], p[8 * s2 + 2 * w + 1] - back[1]);
-            }
+            inc = Mma32<T>::dot2_ones(ph[w], inc);
           }
           pb[s2] = __builtin_bit_cast(short8_t, uint4{ph[0], ph[1], ph[2], ph[3]});
-          if constexpr (PSPLIT) pbl[s2] = __builtin_bit_cast(short8_t, uint4{pl[0], pl[1], pl[2], pl[3]});
         }
         return inc;
       };
       // From the half's row maximum: a new offset when the maximum grew by
       // more than 2^8 over the current one (the accumulators and the sum
       // rescaled), then the probabilities against it; c_in follows.
-      auto softmax_slow = [&](float16v& s, short8_t (&pb)[2], short8_t (&pbl)[2]) {
+      auto softmax_slow = [&](float16v& s, short8_t (&pb)[2]) {
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
@@ -601,28 +599,24 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
           m_c = m_new;
         }
         const float m_eff = m_c == -INFINITY ? 0.f : m_c;
-        const float inc = make_p(s, c_in - m_eff, std::true_type{}, pb, pbl);
+        const float inc = make_p(s, c_in - m_eff, std::true_type{}, pb);
         c_in = m_eff;
         neg_c = float16v{} - m_eff;
         return inc;
       };
       // A half's softmax with `work` (MFMAs of this wave that do not depend
-      // on it) in the same block. bf16 halves first try the current offset
-      // with no row maximum (the scores already carry it): a lane's 16
+      // on it) in the same block. A half first tries the current offset with
+      // no row maximum (the scores already carry it): a lane's 16
       // probabilities summing to at most 2^12 keep each below 2^12, which
-      // the accumulators hold; otherwise (a maximum that grew, an unset
-      // offset, NaN) the half is redone from its maximum.
-      auto softmax_with = [&](float16v& s, short8_t (&pb)[2], short8_t (&pbl)[2], auto&& work) {
-        float inc = 0.f;
-        bool done = false;
+      // bf16 and fp16 P and the accumulators hold; otherwise (a maximum that
+      // grew, an unset offset, NaN) the half is redone from its maximum.
+      auto softmax_with = [&](float16v& s, short8_t (&pb)[2], auto&& work) {
         work();
-        if constexpr (!PSPLIT) {
-          // Speculative: the probabilities are formed in the same block as
-          // `work`, and kept only when every lane has an offset.
-          inc = make_p(s, 0.f, std::false_type{}, pb, pbl);
-          done = !__ballot(m_c == -INFINITY || !(inc <= 4096.f));
-        }
-        if (!done) inc = softmax_slow(s, pb, pbl);
+        // Speculative: the probabilities are formed in the same block as
+        // `work`, and kept only when every lane has an offset.
+        float inc = make_p(s, 0.f, std::false_type{}, pb);
+        const bool done = !__ballot(m_c == -INFINITY || !(inc <= 4096.f));
+        if (!done) inc = softmax_slow(s, pb);
         return inc;
       };
 
@@ -647,8 +641,8 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         asm volatile("");
         mask(0, s0);
       }
-      short8_t pb0[2], pbl0[2];
-      l += softmax_with(s0, pb0, pbl0, [] {});
+      short8_t pb0[2];
+      l += softmax_with(s0, pb0, [] {});
       __builtin_amdgcn_sched_barrier(0);
       {
         short8_t kf[8];
@@ -663,13 +657,13 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
         mask(1, s1);
       }
       // softmax(1) beside P.V(0).
-      short8_t pb1[2], pbl1[2];
-      l += softmax_with(s1, pb1, pbl1, [&] { pv_mma(vf, pb0, pbl0); });
+      short8_t pb1[2];
+      l += softmax_with(s1, pb1, [&] { pv_mma(vf, pb0); });
       __builtin_amdgcn_sched_barrier(0);
       read_v1(1, 0, vf[0]);
       read_v1(1, 1, vf[1]);
       __builtin_amdgcn_sched_barrier(0);
-      pv_mma(vf, pb1, pbl1);
+      pv_mma(vf, pb1);
       __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt<0>();
       if (tl + 1 < nt) fix_v(tl + 1, stage ^ 1);
@@ -735,10 +729,10 @@ __device__ __forceinline__ void prefill_body(const AttnArgs& a, int32_t lg_tok, 
     }
 }
 
-template <typename T, bool PSPLIT>
+template <typename T>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_tok) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  prefill_body<T, PSPLIT>(a, lg_tok, smem, blockIdx.x);
+  prefill_body<T>(a, lg_tok, smem, blockIdx.x);
 }
 
 // The one-launch attention step: the decode and prefill workgroups of a
@@ -752,14 +746,14 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(AttnArgs a, int32_t lg_
 static_assert(kStepDecodeWaves * 2 * 2 * dec::kTileBytes <= kLdsBytes,
               "the step kernel's LDS must hold the decode kernel's tiles");
 
-template <typename T, bool PSPLIT>
+template <typename T>
 __global__ __launch_bounds__(256, 2) void attention_step_kernel(AttnArgs a, int32_t lg_tok, uint32_t first,
                                                                int32_t prefill_first) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t b = blockIdx.x;
   const bool lead = b < first;
   const uint32_t wg = lead ? b : b - first;
-  if (lead == (prefill_first != 0)) prefill_body<T, PSPLIT>(a, lg_tok, smem, wg);
+  if (lead == (prefill_first != 0)) prefill_body<T>(a, lg_tok, smem, wg);
   else dec::decode_split_lds_body<T, 2>(a, smem, wg, kStepDecodeWaves);
 }
 
@@ -768,7 +762,7 @@ __global__ __launch_bounds__(kItemThreads) void prefill_items_kernel(AttnArgs a,
 }
 
 
-template <typename T, bool PSPLIT>
+template <typename T>
 int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   const int lg_tok = prefill_lg_tok(a);
   const int64_t nblk = a.num_tokens / (int64_t{1} << lg_tok) + a.num_requests;
@@ -782,18 +776,18 @@ int launch_prefill_t(const AttnArgs& a, hipStream_t s, hipEvent_t start, hipEven
   }
   static bool raised = false;  // per instantiation; the attribute is process-wide
   if (!raised) {
-    MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<T, PSPLIT>),
+    MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<T>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(kLdsBytes)));
     raised = true;
   }
-  hipExtLaunchKernelGGL(prefill_kernel<T, PSPLIT>, dim3(static_cast<unsigned>(blocks)), dim3(256),
+  hipExtLaunchKernelGGL(prefill_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256),
                         kLdsBytes, s, start, stop, 0, a, lg_tok);
   MVLLM_LAUNCH_CHECK("prefill_kernel");
   return MVLLM_OK;
 }
 
-template <typename T, bool PSPLIT>
+template <typename T>
 int launch_step_t(const AttnArgs& a, bool prefill_first, hipStream_t s, hipEvent_t start, hipEvent_t stop) {
   const int lg_tok = prefill_lg_tok(a);
   const int64_t prefill_blocks = (a.num_tokens / (int64_t{1} << lg_tok) + a.num_requests) * a.num_kv_heads;
@@ -810,12 +804,12 @@ int launch_step_t(const AttnArgs& a, bool prefill_first, hipStream_t s, hipEvent
   }
   static bool raised = false;  // per instantiation; the attribute is process-wide
   if (!raised) {
-    MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_step_kernel<T, PSPLIT>),
+    MVLLM_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(attention_step_kernel<T>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(kLdsBytes)));
     raised = true;
   }
-  hipExtLaunchKernelGGL(attention_step_kernel<T, PSPLIT>, dim3(static_cast<unsigned>(blocks)), dim3(256),
+  hipExtLaunchKernelGGL(attention_step_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256),
                         kLdsBytes, s, start, stop, 0, a, lg_tok, static_cast<uint32_t>(first),
                         prefill_first ? 1 : 0);
   MVLLM_LAUNCH_CHECK("attention_step_kernel");
@@ -853,10 +847,10 @@ int launch_prefill(const AttnArgs& a, int32_t dtype, hipStream_t s, hipEvent_t s
                    hipEvent_t stop) {
   if (!prefill_supported(a, dtype))
     return fail(MVLLM_ERR_UNSUPPORTED, "prefill kernel does not support this geometry");
-  // bf16 keeps P in bf16 (as the reference's Triton kernel keeps it in its
-  // input type); fp16 carries P as a hi/lo pair to meet fp16 tolerances.
-  if (dtype == MVLLM_DTYPE_BF16) return launch_prefill_t<bf16_t, false>(a, s, start, stop);
-  return launch_prefill_t<f16_t, true>(a, s, start, stop);
+  // P is kept in the input type, as the reference's Triton kernel keeps it
+  // (triton_paged.py:271-277).
+  if (dtype == MVLLM_DTYPE_BF16) return launch_prefill_t<bf16_t>(a, s, start, stop);
+  return launch_prefill_t<f16_t>(a, s, start, stop);
 }
 
 int launch_step(const AttnArgs& a, int32_t dtype, bool prefill_first, hipStream_t s, hipEvent_t start,
@@ -865,8 +859,8 @@ int launch_step(const AttnArgs& a, int32_t dtype, bool prefill_first, hipStream_
     return fail(MVLLM_ERR_UNSUPPORTED, "the attention step kernel does not support this geometry");
   if (a.width * a.block_size > INT32_MAX || a.num_tokens > INT32_MAX)
     return fail(MVLLM_ERR_UNSUPPORTED, "decode positions beyond 2^31 are not supported");
-  int rc = dtype == MVLLM_DTYPE_BF16 ? launch_step_t<bf16_t, false>(a, prefill_first, s, start, stop)
-                                     : launch_step_t<f16_t, true>(a, prefill_first, s, start, stop);
+  int rc = dtype == MVLLM_DTYPE_BF16 ? launch_step_t<bf16_t>(a, prefill_first, s, start, stop)
+                                     : launch_step_t<f16_t>(a, prefill_first, s, start, stop);
   if (rc) return rc;
   return launch_decode_combine(a, dtype, s);
 }
