@@ -22,7 +22,8 @@ Reported (one JSON line on stdout):
   the 2.5 PFLOP/s bf16 peak (serial pass), and the mixed step's time with
   the decode and prefill workgroups in one step kernel, also as a fraction
   of its floor max(step bytes / HBM peak, prefill FLOPs / bf16 peak)
-  (``prefill.mixed_step_roofline``);
+  (``prefill.mixed_step_roofline``); ``prefill.fp16`` times the prefill
+  kernel on the same batch in fp16, the reference Triton backend's dtype;
   ``prefill.library`` times the same chunks through PyTorch-ROCm's flash
   attention (variable-length, one launch) and a square bf16 GEMM through
   hipBLASLt on the same GPU;
@@ -1134,6 +1135,21 @@ def main() -> int:
         del mixed_out
         if not args.no_cpu_baseline:
             record["cpu_baseline"] = cpu_prefill_baseline(mixed)
+        # The same batch in fp16, the only dtype of the reference's Triton
+        # backend (dense fp16 MFMA peak = the bf16 one).
+        mixed16 = workloads.llama3_mixed(device, dtype=torch.float16)
+        serial16 = time_attention(
+            mixed16, hip, device, args.steps, args.warmup, concurrent=False, settle_ms=args.settle_ms
+        )
+        fp16 = prefill_record(mixed16, serial16)
+        record["fp16"] = {
+            "kernel": "prefill_kernel<fp16>",
+            "kernel_us": fp16.get("kernel_us"),
+            "achieved": fp16.get("achieved"),
+            "frac": fp16.get("frac"),
+        }
+        del mixed16
+        torch.cuda.empty_cache()
         result["prefill"] = record
         kv = time_kv_write(mixed, hip, device, args.steps, args.warmup, settle_ms=args.settle_ms)
         kv["workload"] = f"llama3_mixed: the step's {kv['tokens']:,} tokens (8 KV heads, head_dim 128, bf16)"
