@@ -1,10 +1,14 @@
-// Any-shape ragged paged attention: one wavefront per (token, query head).
+// Any-shape ragged paged attention: one workgroup of four waves per (token,
+// query head).
 //
 // This kernel carries the shapes the specialised kernels do not (fp32,
 // head_dim other than 128, query-head groups above 16, non-contiguous
-// rows): lanes walk 64 keys at a time, each lane scoring one key, then
-// accumulate P.V with lanes spread over head_dim. Online softmax in fp32
-// (exp2 domain) in the manner of FlashAttention-2 (Dao, 2023).
+// rows): each wave walks every fourth block of 64 keys, each lane scoring
+// one key, then accumulates P.V with lanes spread over head_dim. Online
+// softmax in fp32 (exp2 domain) in the manner of FlashAttention-2 (Dao,
+// 2023); the four waves' partial states are merged through LDS at the end,
+// so a long visible range costs a quarter of the dependent memory round
+// trips of one wave walking it alone.
 #include <cmath>
 
 #include "attention.h"
@@ -13,6 +17,7 @@ namespace mvllm {
 namespace {
 
 constexpr int kMaxDimPerLane = 8;  // head_dim <= 512
+constexpr int kGenericWaves = 4;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -26,6 +31,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// The 16 bytes at p (16-byte aligned) as 16 / sizeof(T) floats.
+template <typename T>
+__device__ __forceinline__ void load16(const T* p, float (&f)[16 / sizeof(T)]) {
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(ws[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = Elem<T>::from_bits(ws[i] & 0xFFFFu);
+      f[2 * i + 1] = Elem<T>::from_bits(ws[i] >> 16);
+    }
+  }
+}
+
 // Largest i in [0, R] with qsl[i] <= t (qsl is non-decreasing).
 __device__ __forceinline__ int64_t request_of(const AttnArgs& a, int64_t t) {
   int64_t lo = 0, hi = a.num_requests;
@@ -37,10 +59,11 @@ __device__ __forceinline__ int64_t request_of(const AttnArgs& a, int64_t t) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(AttnArgs a) {
   const int64_t t = blockIdx.x;
   const int hq = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int D = a.head_dim;
   T* out = static_cast<T*>(a.out) + t * a.o_s0 + static_cast<int64_t>(hq) * a.o_s1;
 
@@ -48,7 +71,7 @@ __global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
   const bool covered = r < a.num_requests && a.qsl[r] <= t && t < a.qsl[r + 1];
   if (!covered) {
     if (a.mode == 0)
-      for (int d = lane; d < D; d += 64) Elem<T>::store(out + d * a.o_s2, 0.f);
+      for (int d = threadIdx.x; d < D; d += 64 * kGenericWaves) Elem<T>::store(out + d * a.o_s2, 0.f);
     return;
   }
   const int64_t qs = a.qsl[r];
@@ -56,7 +79,7 @@ __global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
 
   __shared__ float qsh[64 * kMaxDimPerLane];
   const T* q = static_cast<const T*>(a.q) + t * a.q_s0 + static_cast<int64_t>(hq) * a.q_s1;
-  for (int d = lane; d < D; d += 64) qsh[d] = Elem<T>::load(q + d * a.q_s2) * a.scale_log2;
+  for (int d = threadIdx.x; d < D; d += 64 * kGenericWaves) qsh[d] = Elem<T>::load(q + d * a.q_s2) * a.scale_log2;
   __syncthreads();
 
   int64_t lo, hi;
@@ -67,8 +90,14 @@ __global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < kMaxDimPerLane; ++j) acc[j] = 0.f;
   float m = -INFINITY, l = 0.f;
+  // Key rows contiguous and 16-byte aligned: each lane reads its row in
+  // 16-byte pieces (a quarter or an eighth of the load instructions, each
+  // of which touches one cache line per lane).
+  constexpr int kVec = 16 / static_cast<int>(sizeof(T));
+  const bool vec_rows = a.c_s[4] == 1 && D % kVec == 0 && a.c_s[1] % kVec == 0 && a.c_s[2] % kVec == 0 &&
+                        a.c_s[3] % kVec == 0 && (reinterpret_cast<uintptr_t>(a.cache) & 15u) == 0;
 
-  for (int64_t base = lo; base <= hi; base += 64) {
+  for (int64_t base = lo + 64 * wave; base <= hi; base += 64 * kGenericWaves) {
     const int64_t p = base + lane;
     int64_t row = -1;  // element offset of this lane's key row
     if (p <= hi) {
@@ -76,11 +105,38 @@ __global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
       if (b >= 0)
         row = b * a.c_s[1] + (p % a.block_size) * a.c_s[2] + static_cast<int64_t>(kvh) * a.c_s[3];
     }
+    // Four independent partial sums, so a lane keeps several loads of its
+    // key row in flight instead of one chain of dependent ones.
     float s = -INFINITY;
     if (row >= 0) {
-      float dot = 0.f;
-      for (int d = 0; d < D; ++d) dot += qsh[d] * Elem<T>::load(cache + row + d * a.c_s[4]);
-      s = dot;
+      const T* kp = cache + row;
+      const int64_t ks = a.c_s[4];
+      float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+      int d = 0;
+      if (vec_rows) {
+#pragma unroll 8
+        for (; d < D; d += kVec) {
+          float f[kVec];
+          load16(kp + d, f);
+#pragma unroll
+          for (int e = 0; e < kVec; e += 4) {
+            d0 = __builtin_fmaf(qsh[d + e], f[e], d0);
+            d1 = __builtin_fmaf(qsh[d + e + 1], f[e + 1], d1);
+            d2 = __builtin_fmaf(qsh[d + e + 2], f[e + 2], d2);
+            d3 = __builtin_fmaf(qsh[d + e + 3], f[e + 3], d3);
+          }
+        }
+      } else {
+#pragma unroll 8
+        for (; d + 4 <= D; d += 4) {
+          d0 = __builtin_fmaf(qsh[d], Elem<T>::load(kp + d * ks), d0);
+          d1 = __builtin_fmaf(qsh[d + 1], Elem<T>::load(kp + (d + 1) * ks), d1);
+          d2 = __builtin_fmaf(qsh[d + 2], Elem<T>::load(kp + (d + 2) * ks), d2);
+          d3 = __builtin_fmaf(qsh[d + 3], Elem<T>::load(kp + (d + 3) * ks), d3);
+        }
+        for (; d < D; ++d) d0 = __builtin_fmaf(qsh[d], Elem<T>::load(kp + d * ks), d0);
+      }
+      s = (d0 + d1) + (d2 + d3);
     }
     const float mn = fmaxf(m, wave_max(s));
     const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
@@ -88,24 +144,62 @@ __global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
     l = l * alpha + wave_sum(pr);
 #pragma unroll
     for (int j = 0; j < kMaxDimPerLane; ++j) acc[j] *= alpha;
+    // P.V without a branch per key, so the loads of several keys overlap:
+    // a key with no row reads row 0 of the V plane and adds nothing (a
+    // select, not a product with 0, so a non-finite stale value stays out).
     const int count = static_cast<int>(hi - base + 1 < 64 ? hi - base + 1 : 64);
+#pragma unroll 16
     for (int k = 0; k < count; ++k) {
       const int64_t vrow = __shfl(row, k, 64);
       const float pk = __shfl(pr, k, 64);
-      if (vrow < 0) continue;
+      const bool has = vrow >= 0;
+      const T* vp = cache + a.c_s[0] + (has ? vrow : 0);
 #pragma unroll
       for (int j = 0; j < kMaxDimPerLane; ++j) {
         const int d = lane + 64 * j;
-        if (d < D) acc[j] += pk * Elem<T>::load(cache + a.c_s[0] + vrow + d * a.c_s[4]);
+        if (d < D) {
+          const float pv = pk * Elem<T>::load(vp + d * a.c_s[4]);
+          acc[j] += has ? pv : 0.f;
+        }
       }
     }
     m = mn;
   }
-  const float inv = 1.f / l;  // an empty visible range gives 0/0 = NaN, as the reference's softmax does
+  // Merge the waves' (offset, sum, accumulator) states; a wave that saw no
+  // key holds (-inf, 0, 0) and weighs nothing.
+  __shared__ float msh[kGenericWaves], lsh[kGenericWaves];
+  __shared__ float accsh[kGenericWaves][64 * kMaxDimPerLane];
+  if (lane == 0) {
+    msh[wave] = m;
+    lsh[wave] = l;
+  }
 #pragma unroll
   for (int j = 0; j < kMaxDimPerLane; ++j) {
     const int d = lane + 64 * j;
-    if (d < D) Elem<T>::store(out + d * a.o_s2, acc[j] * inv);
+    if (d < D) accsh[wave][d] = acc[j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kGenericWaves; ++w) mx = fmaxf(mx, msh[w]);
+  float weight[kGenericWaves];
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kGenericWaves; ++w) {
+    weight[w] = msh[w] == -INFINITY ? 0.f : exp2f(msh[w] - mx);
+    total += weight[w] * lsh[w];
+  }
+  const float inv = 1.f / total;  // an empty visible range gives 0/0 = NaN, as the reference's softmax does
+#pragma unroll
+  for (int j = 0; j < kMaxDimPerLane; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGenericWaves; ++w) o += weight[w] * accsh[w][d];
+      Elem<T>::store(out + d * a.o_s2, o * inv);
+    }
   }
 }
 
@@ -120,13 +214,13 @@ int launch_generic(const AttnArgs& a, int32_t dtype, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.num_tokens), static_cast<unsigned>(a.num_q_heads));
   switch (dtype) {
     case MVLLM_DTYPE_F32:
-      hipLaunchKernelGGL(attention_generic_kernel<float>, grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL(attention_generic_kernel<float>, grid, dim3(64 * kGenericWaves), 0, s, a);
       break;
     case MVLLM_DTYPE_F16:
-      hipLaunchKernelGGL(attention_generic_kernel<f16_t>, grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL(attention_generic_kernel<f16_t>, grid, dim3(64 * kGenericWaves), 0, s, a);
       break;
     case MVLLM_DTYPE_BF16:
-      hipLaunchKernelGGL(attention_generic_kernel<bf16_t>, grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL(attention_generic_kernel<bf16_t>, grid, dim3(64 * kGenericWaves), 0, s, a);
       break;
     default:
       return fail(MVLLM_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
