@@ -672,6 +672,53 @@ def test_qwen3_decode_batch_whole(device):
     check_whole_batch(w, out, group=64)
 
 
+# ------------------------------------------------------ seeded random batches
+
+RANDOM_LAYOUTS = [(16, 8, 128), (32, 8, 128), (8, 8, 128), (16, 2, 128), (64, 4, 128), (12, 4, 128), (16, 8, 64),
+                  (8, 2, 96)]
+
+
+def random_batch(seed: int):
+    """Draw one ragged batch: head layout, block size, dtype, spec, 1-10
+    requests, each a decode or a prefill chunk at a random prior context,
+    and whether the max_query_len hint is given."""
+
+    rng = np.random.default_rng(1000 + seed)
+    hq, hkv, d = RANDOM_LAYOUTS[rng.integers(len(RANDOM_LAYOUTS))]
+    bs = int(rng.choice([16, 16, 32, 8, 64]))
+    dtype = [torch.bfloat16, torch.float16][rng.integers(2)]
+    spec = [None, None, None, SlidingWindowSpec(int(rng.integers(1, 400))), ChunkedLocalSpec(int(rng.choice([16, 64, 250])))][
+        rng.integers(5)
+    ]
+    nreq = int(rng.integers(1, 11))
+    lengths, qlens = [], []
+    for _ in range(nreq):
+        ql = 1 if rng.random() < 0.5 else int(rng.integers(2, 301))
+        prior = int(rng.integers(0, 3001))
+        lengths.append(prior + ql)
+        qlens.append(ql)
+    hint = bool(rng.integers(2))
+    return dtype, hq, hkv, d, bs, spec, lengths, qlens, hint
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_ragged_batches(device, seed):
+    """Seeded random batches across head layouts (the specialised kernels'
+    group sizes, a group of 3 and head_dim 64 / 96 on the generic kernel),
+    block sizes 8-64, bf16 / fp16, full, sliding-window and chunked-local
+    specs, decodes and prefill chunks at prior contexts up to 3,000, with
+    and without the max_query_len hint: the cache bit-exact, every output
+    row against the oracle."""
+
+    dtype, hq, hkv, d, bs, spec, lengths, qlens, hint = random_batch(seed)
+    q, k, v, cache, md = build_case(device, dtype, lengths, qlens, hq, hkv, d, bs, spec=spec, seed=seed)
+    if hint:
+        md = dataclasses.replace(md, max_query_len=max(qlens))
+    print(f"seed {seed}: {dtype} heads {hq}/{hkv} d {d} block {bs} spec {spec} qlens {qlens} lengths {lengths} "
+          f"hint {hint}", flush=True)
+    run_and_check(q, k, v, cache, md, dtype)
+
+
 # ------------------------------------------------- shared prefix (prefix cache)
 
 
