@@ -54,7 +54,7 @@ Other workloads: ``llama3_mixed``, ``llama3_long_decode``, ``llama3_long_prefill
 causal chunks of 4,096 from position 0) (attention steps),
 ``qwen3_e2e`` and ``llama3_e2e`` (end-to-end generation; the Llama-3-8B one
 shares a 4,096-token prefix through the prefix cache and holds a ~200 GB KV
-cache).
+cache), and ``small_mixed`` (the ``config1`` record alone).
 """
 
 from __future__ import annotations
@@ -931,6 +931,7 @@ def main() -> int:
             "llama3_long_decode",
             "qwen3_e2e",
             "llama3_e2e",
+            "small_mixed",
         ],
     )
     parser.add_argument(
@@ -996,6 +997,13 @@ def main() -> int:
     device = torch.device("cuda", 0)
     if args.workload in E2E_CONFIGS:
         print(json.dumps(e2e_line(args, device)), flush=True)
+        return 0
+    if args.workload == "small_mixed":
+        # The config-1 record alone (fp32 and bf16 forwards, the CPU path beside them).
+        line = {"metric": "forward latency, contexts [17, 64, 130, 255]", "unit": "us", "higher_is_better": False,
+                "n_gpus": 1, "data": "synthetic"}
+        line.update(small_mixed_record(HipEvents(), device))
+        print(json.dumps(line), flush=True)
         return 0
 
     w, description = attention_workload(args.workload, device)

@@ -4,7 +4,10 @@
 // This kernel carries the shapes the specialised kernels do not (fp32,
 // head_dim other than 128, query-head groups above 16, non-contiguous
 // rows): each wave walks every fourth block of 64 keys, each lane scoring
-// one key, then accumulates P.V with lanes spread over head_dim. Online
+// one key, then accumulates P.V with lanes spread over head_dim (one
+// instantiation per bound of 64, 128, 256 and 512 elements, so the loops
+// over a lane's elements and over a block's keys unroll without guards on
+// elements past head_dim's bound). Online
 // softmax in fp32 (exp2 domain) in the manner of FlashAttention-2 (Dao,
 // 2023); the four waves' partial states are merged through LDS at the end,
 // so a long visible range costs a quarter of the dependent memory round
@@ -58,7 +61,8 @@ __device__ __forceinline__ int64_t request_of(const AttnArgs& a, int64_t t) {
   return lo;
 }
 
-template <typename T>
+// DPL: head_dim elements per lane in the P.V accumulation (head_dim <= 64 * DPL).
+template <typename T, int DPL>
 __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(AttnArgs a) {
   const int64_t t = blockIdx.x;
   const int hq = blockIdx.y;
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   const int64_t qs = a.qsl[r];
   if (a.mode == 1 && a.qsl[r + 1] - qs == 1) return;
 
-  __shared__ float qsh[64 * kMaxDimPerLane];
+  __shared__ float qsh[64 * DPL];
   const T* q = static_cast<const T*>(a.q) + t * a.q_s0 + static_cast<int64_t>(hq) * a.q_s1;
   for (int d = threadIdx.x; d < D; d += 64 * kGenericWaves) qsh[d] = Elem<T>::load(q + d * a.q_s2) * a.scale_log2;
   __syncthreads();
@@ -86,9 +90,9 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   visible_range(a, r, qs, t, lo, hi);
   const int kvh = hq / a.group;
   const T* cache = static_cast<const T*>(a.cache);
-  float acc[kMaxDimPerLane];
+  float acc[DPL];
 #pragma unroll
-  for (int j = 0; j < kMaxDimPerLane; ++j) acc[j] = 0.f;
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
   float m = -INFINITY, l = 0.f;
   // Key rows contiguous and 16-byte aligned: each lane reads its row in
   // 16-byte pieces (a quarter or an eighth of the load instructions, each
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
       float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
       int d = 0;
       if (vec_rows) {
-#pragma unroll 8
+#pragma unroll 16
         for (; d < D; d += kVec) {
           float f[kVec];
           load16(kp + d, f);
@@ -143,19 +147,19 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
     const float pr = (s == -INFINITY) ? 0.f : exp2f(s - mn);
     l = l * alpha + wave_sum(pr);
 #pragma unroll
-    for (int j = 0; j < kMaxDimPerLane; ++j) acc[j] *= alpha;
+    for (int j = 0; j < DPL; ++j) acc[j] *= alpha;
     // P.V without a branch per key, so the loads of several keys overlap:
     // a key with no row reads row 0 of the V plane and adds nothing (a
     // select, not a product with 0, so a non-finite stale value stays out).
     const int count = static_cast<int>(hi - base + 1 < 64 ? hi - base + 1 : 64);
-#pragma unroll 16
+#pragma unroll 32
     for (int k = 0; k < count; ++k) {
       const int64_t vrow = __shfl(row, k, 64);
       const float pk = __shfl(pr, k, 64);
       const bool has = vrow >= 0;
       const T* vp = cache + a.c_s[0] + (has ? vrow : 0);
 #pragma unroll
-      for (int j = 0; j < kMaxDimPerLane; ++j) {
+      for (int j = 0; j < DPL; ++j) {
         const int d = lane + 64 * j;
         if (d < D) {
           const float pv = pk * Elem<T>::load(vp + d * a.c_s[4]);
@@ -168,13 +172,13 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   // Merge the waves' (offset, sum, accumulator) states; a wave that saw no
   // key holds (-inf, 0, 0) and weighs nothing.
   __shared__ float msh[kGenericWaves], lsh[kGenericWaves];
-  __shared__ float accsh[kGenericWaves][64 * kMaxDimPerLane];
+  __shared__ float accsh[kGenericWaves][64 * DPL];
   if (lane == 0) {
     msh[wave] = m;
     lsh[wave] = l;
   }
 #pragma unroll
-  for (int j = 0; j < kMaxDimPerLane; ++j) {
+  for (int j = 0; j < DPL; ++j) {
     const int d = lane + 64 * j;
     if (d < D) accsh[wave][d] = acc[j];
   }
@@ -192,7 +196,7 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   }
   const float inv = 1.f / total;  // an empty visible range gives 0/0 = NaN, as the reference's softmax does
 #pragma unroll
-  for (int j = 0; j < kMaxDimPerLane; ++j) {
+  for (int j = 0; j < DPL; ++j) {
     const int d = lane + 64 * j;
     if (d < D) {
       float o = 0.f;
@@ -203,6 +207,19 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   }
 }
 
+template <typename T>
+int launch_generic_t(const AttnArgs& a, int dpl, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.num_tokens), static_cast<unsigned>(a.num_q_heads));
+  const dim3 block(64 * kGenericWaves);
+  switch (dpl) {
+    case 1: hipLaunchKernelGGL((attention_generic_kernel<T, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attention_generic_kernel<T, 2>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attention_generic_kernel<T, 4>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((attention_generic_kernel<T, 8>), grid, block, 0, s, a); break;
+  }
+  return MVLLM_OK;
+}
+
 }  // namespace
 
 int launch_generic(const AttnArgs& a, int32_t dtype, hipStream_t s) {
@@ -211,20 +228,15 @@ int launch_generic(const AttnArgs& a, int32_t dtype, hipStream_t s) {
   if (a.num_tokens == 0 || a.num_q_heads == 0) return MVLLM_OK;
   if (a.num_tokens > INT32_MAX || a.num_q_heads > 65535)
     return fail(MVLLM_ERR_INVALID, "generic attention grid too large");
-  const dim3 grid(static_cast<unsigned>(a.num_tokens), static_cast<unsigned>(a.num_q_heads));
+  const int dpl = a.head_dim <= 64 ? 1 : a.head_dim <= 128 ? 2 : a.head_dim <= 256 ? 4 : 8;
+  int rc = MVLLM_OK;
   switch (dtype) {
-    case MVLLM_DTYPE_F32:
-      hipLaunchKernelGGL(attention_generic_kernel<float>, grid, dim3(64 * kGenericWaves), 0, s, a);
-      break;
-    case MVLLM_DTYPE_F16:
-      hipLaunchKernelGGL(attention_generic_kernel<f16_t>, grid, dim3(64 * kGenericWaves), 0, s, a);
-      break;
-    case MVLLM_DTYPE_BF16:
-      hipLaunchKernelGGL(attention_generic_kernel<bf16_t>, grid, dim3(64 * kGenericWaves), 0, s, a);
-      break;
-    default:
-      return fail(MVLLM_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    case MVLLM_DTYPE_F32: rc = launch_generic_t<float>(a, dpl, s); break;
+    case MVLLM_DTYPE_F16: rc = launch_generic_t<f16_t>(a, dpl, s); break;
+    case MVLLM_DTYPE_BF16: rc = launch_generic_t<bf16_t>(a, dpl, s); break;
+    default: return fail(MVLLM_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
   }
+  if (rc) return rc;
   MVLLM_LAUNCH_CHECK("attention_generic_kernel");
   return MVLLM_OK;
 }
