@@ -1,17 +1,19 @@
-// Any-shape ragged paged attention: one workgroup of four waves per (token,
+// Any-shape ragged paged attention: one workgroup of W waves per (token,
 // query head).
 //
 // This kernel carries the shapes the specialised kernels do not (fp32,
 // head_dim other than 128, query-head groups above 16, non-contiguous
-// rows): each wave walks every fourth block of 64 keys, each lane scoring
+// rows): each wave walks every W-th block of 64 keys, each lane scoring
 // one key, then accumulates P.V with lanes spread over head_dim (one
 // instantiation per bound of 64, 128, 256 and 512 elements, so the loops
 // over a lane's elements and over a block's keys unroll without guards on
-// elements past head_dim's bound). Online
-// softmax in fp32 (exp2 domain) in the manner of FlashAttention-2 (Dao,
-// 2023); the four waves' partial states are merged through LDS at the end,
-// so a long visible range costs a quarter of the dependent memory round
-// trips of one wave walking it alone.
+// elements past head_dim's bound). Online softmax in fp32 (exp2 domain) in
+// the manner of FlashAttention-2 (Dao, 2023); the waves' partial states are
+// merged through LDS at the end, so a long visible range costs 1/W of the
+// dependent memory round trips of one wave walking it alone. W is 4 when
+// the block table reaches at most 1,024 keys (more waves would find no
+// block to walk) and 16 beyond (8 for head_dim above 128, whose
+// accumulators do not fit the register share of 16 waves).
 #include <cmath>
 
 #include "attention.h"
@@ -20,7 +22,6 @@ namespace mvllm {
 namespace {
 
 constexpr int kMaxDimPerLane = 8;  // head_dim <= 512
-constexpr int kGenericWaves = 4;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -61,9 +62,10 @@ __device__ __forceinline__ int64_t request_of(const AttnArgs& a, int64_t t) {
   return lo;
 }
 
-// DPL: head_dim elements per lane in the P.V accumulation (head_dim <= 64 * DPL).
-template <typename T, int DPL>
-__global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(AttnArgs a) {
+// DPL: head_dim elements per lane in the P.V accumulation (head_dim <= 64 * DPL);
+// WAVES: waves per workgroup, each walking every WAVES-th block of 64 keys.
+template <typename T, int DPL, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attention_generic_kernel(AttnArgs a) {
   const int64_t t = blockIdx.x;
   const int hq = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   const bool covered = r < a.num_requests && a.qsl[r] <= t && t < a.qsl[r + 1];
   if (!covered) {
     if (a.mode == 0)
-      for (int d = threadIdx.x; d < D; d += 64 * kGenericWaves) Elem<T>::store(out + d * a.o_s2, 0.f);
+      for (int d = threadIdx.x; d < D; d += 64 * WAVES) Elem<T>::store(out + d * a.o_s2, 0.f);
     return;
   }
   const int64_t qs = a.qsl[r];
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
 
   __shared__ float qsh[64 * DPL];
   const T* q = static_cast<const T*>(a.q) + t * a.q_s0 + static_cast<int64_t>(hq) * a.q_s1;
-  for (int d = threadIdx.x; d < D; d += 64 * kGenericWaves) qsh[d] = Elem<T>::load(q + d * a.q_s2) * a.scale_log2;
+  for (int d = threadIdx.x; d < D; d += 64 * WAVES) qsh[d] = Elem<T>::load(q + d * a.q_s2) * a.scale_log2;
   __syncthreads();
 
   int64_t lo, hi;
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   const bool vec_rows = a.c_s[4] == 1 && D % kVec == 0 && a.c_s[1] % kVec == 0 && a.c_s[2] % kVec == 0 &&
                         a.c_s[3] % kVec == 0 && (reinterpret_cast<uintptr_t>(a.cache) & 15u) == 0;
 
-  for (int64_t base = lo + 64 * wave; base <= hi; base += 64 * kGenericWaves) {
+  for (int64_t base = lo + 64 * wave; base <= hi; base += 64 * WAVES) {
     const int64_t p = base + lane;
     int64_t row = -1;  // element offset of this lane's key row
     if (p <= hi) {
@@ -171,8 +173,8 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   }
   // Merge the waves' (offset, sum, accumulator) states; a wave that saw no
   // key holds (-inf, 0, 0) and weighs nothing.
-  __shared__ float msh[kGenericWaves], lsh[kGenericWaves];
-  __shared__ float accsh[kGenericWaves][64 * DPL];
+  __shared__ float msh[WAVES], lsh[WAVES];
+  __shared__ float accsh[WAVES][64 * DPL];
   if (lane == 0) {
     msh[wave] = m;
     lsh[wave] = l;
@@ -186,11 +188,11 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
   if (wave != 0) return;
   float mx = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kGenericWaves; ++w) mx = fmaxf(mx, msh[w]);
-  float weight[kGenericWaves];
+  for (int w = 0; w < WAVES; ++w) mx = fmaxf(mx, msh[w]);
+  float weight[WAVES];
   float total = 0.f;
 #pragma unroll
-  for (int w = 0; w < kGenericWaves; ++w) {
+  for (int w = 0; w < WAVES; ++w) {
     weight[w] = msh[w] == -INFINITY ? 0.f : exp2f(msh[w] - mx);
     total += weight[w] * lsh[w];
   }
@@ -201,21 +203,26 @@ __global__ __launch_bounds__(64 * kGenericWaves) void attention_generic_kernel(A
     if (d < D) {
       float o = 0.f;
 #pragma unroll
-      for (int w = 0; w < kGenericWaves; ++w) o += weight[w] * accsh[w][d];
+      for (int w = 0; w < WAVES; ++w) o += weight[w] * accsh[w][d];
       Elem<T>::store(out + d * a.o_s2, o * inv);
     }
   }
 }
 
+template <typename T, int DPL, int WAVES>
+void launch_generic_w(const AttnArgs& a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.num_tokens), static_cast<unsigned>(a.num_q_heads));
+  hipLaunchKernelGGL((attention_generic_kernel<T, DPL, WAVES>), grid, dim3(64 * WAVES), 0, s, a);
+}
+
 template <typename T>
 int launch_generic_t(const AttnArgs& a, int dpl, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(a.num_tokens), static_cast<unsigned>(a.num_q_heads));
-  const dim3 block(64 * kGenericWaves);
+  const bool long_reach = a.width * a.block_size > 1024;
   switch (dpl) {
-    case 1: hipLaunchKernelGGL((attention_generic_kernel<T, 1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attention_generic_kernel<T, 2>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attention_generic_kernel<T, 4>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((attention_generic_kernel<T, 8>), grid, block, 0, s, a); break;
+    case 1: long_reach ? launch_generic_w<T, 1, 16>(a, s) : launch_generic_w<T, 1, 4>(a, s); break;
+    case 2: long_reach ? launch_generic_w<T, 2, 16>(a, s) : launch_generic_w<T, 2, 4>(a, s); break;
+    case 4: long_reach ? launch_generic_w<T, 4, 8>(a, s) : launch_generic_w<T, 4, 4>(a, s); break;
+    default: long_reach ? launch_generic_w<T, 8, 8>(a, s) : launch_generic_w<T, 8, 4>(a, s); break;
   }
   return MVLLM_OK;
 }

@@ -178,15 +178,20 @@ def test_ragged_multi_request_with_arbitrary_starts(device, dtype, hq, hkv, d):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize(("hq", "hkv", "d", "bs"), [(8, 2, 64, 16), (6, 2, 96, 8), (12, 4, 256, 32)],
-                         ids=["d64", "d96-bs8", "d256-bs32"])
-def test_generic_kernel_long_ranges_over_four_waves(device, dtype, hq, hkv, d, bs):
-    """Shapes only the generic kernel takes (fp32; head_dim 64, 96, 256;
-    block 8): visible ranges of 5 to 4,100 keys, so the four waves of a
-    (token, head) workgroup each walk none, one or many 64-key blocks and
+@pytest.mark.parametrize(
+    ("hq", "hkv", "d", "bs"),
+    [(8, 2, 64, 16), (6, 2, 96, 8), (12, 4, 256, 32), (4, 2, 320, 16), (4, 4, 512, 16)],
+    ids=["d64", "d96-bs8", "d256-bs32", "d320", "d512"],
+)
+@pytest.mark.parametrize("longest", [4100, 1000], ids=["reach-4100", "reach-1000"])
+def test_generic_kernel_ranges_merged_over_waves(device, dtype, hq, hkv, d, bs, longest):
+    """Shapes only the generic kernel takes (fp32; head_dim 64, 96, 256, 320,
+    512; block 8): visible ranges of 5 keys up to ``longest``, so the waves
+    of a (token, head) workgroup (4 when the table reaches at most 1,024
+    keys, 8 or 16 beyond) each walk none, one or many 64-key blocks and
     their states are merged; NaN-sentinel cache slots stay out."""
 
-    lengths, qlens = [5, 300, 1500, 4100, 64], [5, 1, 20, 1, 3]
+    lengths, qlens = [5, 300, min(1500, longest), longest, 64], [5, 1, 20, 1, 3]
     q, k, v, cache, md = build_case(device, dtype, lengths, qlens, hq, hkv, d, bs, seed=97)
     run_and_check(q, k, v, cache, md, dtype)
 
