@@ -707,13 +707,15 @@ def random_batch(seed: int):
 
 
 @pytest.mark.parametrize("seed", range(24))
-def test_random_ragged_batches(device, seed):
+def test_random_ragged_batches(device, monkeypatch, seed):
     """Seeded random batches across head layouts (the specialised kernels'
     group sizes, a group of 3 and head_dim 64 / 96 on the generic kernel),
     block sizes 8-64, bf16 / fp16, full, sliding-window and chunked-local
     specs, decodes and prefill chunks at prior contexts up to 3,000, with
     and without the max_query_len hint: the cache bit-exact, every output
-    row against the oracle."""
+    row against the oracle, and the same outputs bit for bit when the
+    decode and prefill kernels run as separate launches instead of one
+    step kernel."""
 
     dtype, hq, hkv, d, bs, spec, lengths, qlens, hint = random_batch(seed)
     q, k, v, cache, md = build_case(device, dtype, lengths, qlens, hq, hkv, d, bs, spec=spec, seed=seed)
@@ -721,7 +723,12 @@ def test_random_ragged_batches(device, seed):
         md = dataclasses.replace(md, max_query_len=max(qlens))
     print(f"seed {seed}: {dtype} heads {hq}/{hkv} d {d} block {bs} spec {spec} qlens {qlens} lengths {lengths} "
           f"hint {hint}", flush=True)
-    run_and_check(q, k, v, cache, md, dtype)
+    before = cache.clone()
+    out = run_and_check(q, k, v, cache, md, dtype)
+    monkeypatch.setenv("MVLLM_STEP_KERNEL", "0")
+    separate = operator()(q, k, v, before, md)
+    torch.cuda.synchronize()
+    assert torch.equal(separate.view(torch.int16), out.view(torch.int16))
 
 
 # ------------------------------------------------- shared prefix (prefix cache)
